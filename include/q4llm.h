@@ -1,0 +1,199 @@
+/*
+ * q4llm.h -- C ABI of the MI355X (gfx950) int4 LLM hot path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers and sizes (no framework types), owned by the caller;
+ *   - validates all arguments on the host first and returns a negative Q4_ERR_* code without
+ *     touching the device when they are wrong;
+ *   - is stream ordered and asynchronous: it enqueues kernels on `stream` (a hipStream_t, NULL =
+ *     the default stream) and never synchronises the host;
+ *   - allocates no device memory; scratch space is passed in as `workspace`.
+ *
+ * Data formats follow the reference LlamaQ4 module (scripts/llm/llama_q4.py):
+ *   qweight [N, K/8] int32: nibble b (bits 4b..4b+3) of word w holds k = 8w + b, stored as q + 8
+ *                           in [0, 15] (llama_q4.py:25-38);
+ *   scales  [N, K/group] fp16 (bit patterns passed as uint16_t);
+ *   KV caches [max_ctx, n_kv, head_dim] fp16, position-first, written in place (llama_q4.py:222-223).
+ *
+ * dtype codes: Q4_F32 = 0, Q4_F16 = 1.
+ */
+#ifndef Q4LLM_H
+#define Q4LLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  Q4_OK = 0,
+  Q4_ERR_NULL = -1,       /* a required pointer is NULL */
+  Q4_ERR_SHAPE = -2,      /* sizes violate the documented divisibility / range rules */
+  Q4_ERR_ALIGN = -3,      /* a pointer is not aligned as documented */
+  Q4_ERR_DTYPE = -4,      /* unknown or unsupported dtype code */
+  Q4_ERR_WORKSPACE = -5,  /* workspace missing or smaller than the *_workspace_bytes query */
+  Q4_ERR_RANGE = -6,      /* a position / bucket / length is out of range */
+  Q4_ERR_UNSUPPORTED = -7,/* valid request this build does not implement (documented limit) */
+  Q4_ERR_HIP = -100       /* a HIP runtime call failed; q4llm_last_hip_error() has the code */
+};
+
+enum { Q4_F32 = 0, Q4_F16 = 1 };
+
+/* Human-readable text for a status code (static storage). */
+const char* q4llm_status_string(int status);
+/* The hipError_t of the last failed HIP call made by this library on this thread (0 if none). */
+int q4llm_last_hip_error(void);
+/* ABI version of this header: bumped when a signature changes. */
+int q4llm_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * int4 weight format (reference: scripts/llm/llama_q4.py)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Replaces quantize_q4 (llama_q4.py:25-38). w [N, K] fp32 row-major -> qweight [N, K/8] int32 and
+ * scales [N, K/group] fp16. scale = max(amax|w_g|, 1e-8) / 7 in fp32, q = round-half-even(w / scale)
+ * clamped to [-8, 7], stored as q + 8; the scale is cast to fp16 after q is computed.
+ * Requires K % 8 == 0, K % group == 0, group % 8 == 0. Bit-exact with the reference. */
+int q4_quantize(const float* w, int32_t* qweight, uint16_t* scales, int64_t N, int64_t K,
+                int group, void* stream);
+
+/* Replaces unpack_q4 (llama_q4.py:41-45): nibbles [N, K] uint8 in [0, 15]. K % 8 == 0. */
+int q4_unpack(const int32_t* qweight, uint8_t* nibbles, int64_t N, int64_t K, void* stream);
+
+/* Replaces dequantize_q4 (llama_q4.py:48-51): w [N, K] = (nibble - 8) * fp32(scale) written as
+ * w_dtype (Q4_F32 is exact; Q4_F16 rounds to nearest even). */
+int q4_dequant(const int32_t* qweight, const uint16_t* scales, void* w, int w_dtype, int64_t N,
+               int64_t K, int group, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Projections (reference: QLinear.forward / _gemv_fused, llama_q4.py:69-90)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Decode GEMV, replaces QLinear._gemv_fused (llama_q4.py:74-90) and QLinear.forward at M == 1
+ * (llama_q4.py:69-72): y[n] = residual[n] + sum_k x[k] * (nib[n,k] - 8) * scale[n, k/group].
+ * x: K elements of x_dtype; y: N elements of y_dtype; residual: NULL or N fp32 (only with
+ * y_dtype == Q4_F32; may alias y). Accumulation is fp32.
+ * Requires K % 8 == 0, K % group == 0, group % 8 == 0, K <= 16384, 16-byte aligned qweight/x. */
+int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
+            int y_dtype, const float* residual, int64_t N, int64_t K, int group, void* stream);
+
+/* Prefill projection, replaces QLinear.forward at M > 1 (llama_q4.py:72,
+ * F.linear(x, dequantize_q4(W))): y[M, N] = residual + x[M, K] @ dequant(W)^T, x and y fp32.
+ * Runs on the fp16 matrix cores with x split into two fp16 terms and the int4 values exact in
+ * fp16, the group scale applied in fp32 per K-group, so the result carries fp32-level accuracy.
+ * Requires K % 32 == 0, group % 32 == 0, K % group == 0. residual: NULL or [M, N] fp32 (may alias y). */
+int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
+              const float* residual, int64_t N, int64_t K, int group, void* stream);
+
+/* fp16 GEMM C[M,N] = A[M,K] @ B[N,K]^T ("NT", gemm/shapes.py:4-6, S2 prefill_nt), fp32
+ * accumulation, fp16 output, row-major with leading dimensions lda/ldb/ldc (in elements).
+ * Requires K % 8 == 0, lda/ldb % 8 == 0, 16-byte aligned A and B. */
+int gemm_f16_nt(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Attention over a KV bucket (reference: LlamaQ4.step, llama_q4.py:204-232)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Bytes of workspace attn_bucket needs for C query rows, n_q heads, head_dim hd, bucket L. */
+int attn_workspace_bytes(int C, int n_q, int n_kv, int hd, int L, size_t* bytes);
+
+/* GQA attention of C query rows at positions start[0] + c over k_cache/v_cache[:L]
+ * (llama_q4.py:224-232): s = q . k * scale, keys with key_pos > pos masked (the reference's -1e30
+ * fill), softmax in fp32, o = p . v. q [C, n_q, hd] fp32 (RoPE applied), caches
+ * [>= L, n_kv, hd] fp16, out [C, n_q * hd] fp32. `start` is a device int32 (read by the kernels, so
+ * the launch can be replayed from a graph). Split-K over the bucket length with a log-sum-exp
+ * combine. Requires n_q % n_kv == 0, hd in {64, 128}, start + C <= L (checked on the device:
+ * rows past L produce zeros). */
+int attn_bucket(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Element-wise / gather ops of LlamaQ4.step (llama_q4.py:141-142, 194-239)
+ * ------------------------------------------------------------------------------------------- */
+
+/* rms_norm (llama_q4.py:141-142): out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, rows of D fp32.
+ * `row` NULL: all M rows; else the single row row[0] (device int32) of x -> out[0]. */
+int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M, int64_t D, float eps,
+                const int32_t* row, void* stream);
+
+/* RoPE + in-place KV write (llama_q4.py:205-207, 218-223): for c < C, pos = start[0] + c:
+ * q = q*cos[pos] + rotate_half(q)*sin[pos] (in place in qkv), k likewise, then
+ * k_cache[pos] = fp16(k), v_cache[pos] = fp16(v). qkv [C, (n_q + 2 n_kv) * hd] fp32,
+ * cos/sin [max_ctx, hd] fp32. Positions >= max_ctx are skipped (the host checks ranges). */
+int rope_kv_write(float* qkv, const float* cos_t, const float* sin_t, uint16_t* k_cache,
+                  uint16_t* v_cache, int C, int n_q, int n_kv, int hd, int max_ctx,
+                  const int32_t* start, void* stream);
+
+/* SwiGLU (llama_q4.py:236): out[m, i] = silu(gu[m, i]) * gu[m, inter + i], gu [M, 2*inter]. */
+int silu_mul_f32(const float* gu, float* out, int64_t M, int64_t inter, void* stream);
+
+/* QEmbedding.lookup (llama_q4.py:106-119): out[c] = dequant(row tokens[c]) fp32, tokens device
+ * int32 [C]; tokens outside [0, vocab) give a zero row (the reference's `valid` mask). */
+int q4_embed_lookup(const int32_t* qweight, const uint16_t* scales, const int32_t* tokens, float* out,
+                    int C, int64_t vocab, int64_t D, int group, void* stream);
+
+/* torch.argmax(logits, -1) (llama_q4.py:239): first index of the maximum of V fp32 values,
+ * written as int32 to out[0]. workspace >= argmax_workspace_bytes(V). */
+int argmax_workspace_bytes(int64_t V, size_t* bytes);
+int argmax_f32(const float* logits, int64_t V, int32_t* out, void* workspace, size_t workspace_bytes,
+               void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Whole-model step (the exported entry points prefill_c{C}_l{L} / decode_l{L} /
+ * decode_logits_l{L}, scripts/llm/export_llama.py:1-10,35-49; LlamaQ4.step llama_q4.py:199-239)
+ * ------------------------------------------------------------------------------------------- */
+
+typedef struct q4llm_layer {
+  const int32_t* wqkv_q;  const uint16_t* wqkv_s;   /* [(n_q + 2 n_kv) hd, dim] */
+  const int32_t* wo_q;    const uint16_t* wo_s;     /* [dim, n_q hd] */
+  const int32_t* wgu_q;   const uint16_t* wgu_s;    /* [2 inter, dim] (gate rows then up rows) */
+  const int32_t* wdown_q; const uint16_t* wdown_s;  /* [dim, inter] */
+  const float* ln_in;     const float* ln_post;     /* [dim] */
+} q4llm_layer;
+
+typedef struct q4llm_model {
+  int dim, n_layers, n_heads, n_kv, head_dim, inter, vocab, group, max_ctx;
+  float eps;
+  const int32_t* embed_q; const uint16_t* embed_s;  /* tied embedding / LM head [vocab, dim] */
+  const float* ln_f;                                 /* [dim] */
+  const float* cos_t; const float* sin_t;            /* RoPE tables [max_ctx, head_dim] */
+  const q4llm_layer* layers;                         /* host array of n_layers */
+} q4llm_model;
+
+/* Workspace bytes for one step with C tokens and bucket L. */
+int q4llm_step_workspace_bytes(const q4llm_model* m, int C, int L, size_t* bytes);
+
+/* One LlamaQ4.step: tokens [C] int32, start [1], last [1] (device), caches = 2 * n_layers device
+ * pointers (k0, v0, k1, v1, ...) each [max_ctx, n_kv, head_dim] fp16 written in place at
+ * start..start+C-1; attention reads cache[:L]. Writes the greedy next token (int32) to next[0]
+ * and, if logits != NULL, the [vocab] fp32 logits of row `last`. The host checks C, L against
+ * max_ctx; start + C <= L is the caller's schedule contract (llm_runner.c:143-149). */
+int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start,
+               const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Measurement and tuning hooks (counterparts of gemm/roofline.py:27-70 and of the tuner's
+ * candidate timing, scripts/tune/kernel_tuner.py:144-227; not part of the model path)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Streaming read of `bytes` (multiple of 16): workgroups of 256 threads, each thread issuing
+ * loads_per_thread (1, 2, 4 or 8) 16-byte loads up front. sink: one float, never written in practice. */
+int q4_probe_read(const void* buf, int64_t bytes, float* sink, int loads_per_thread, void* stream);
+/* Empty kernel launch (launch-floor probe). */
+int q4_probe_empty(int grid, int block, void* stream);
+/* Number of entries in the explicit GEMV tile list, and q4_gemv with a forced entry (cfg < 0:
+ * automatic) and grid (0: automatic). */
+int q4_gemv_num_configs(void);
+int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
+                int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg, int grid,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q4LLM_H */

@@ -1,0 +1,86 @@
+// Shared definitions of the gfx950 int4 LLM library: status handling, launch helpers and the
+// small device utilities every kernel file uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <type_traits>
+
+#include "q4llm.h"
+
+namespace q4 {
+
+// Records the HIP error for q4llm_last_hip_error() and maps it to Q4_ERR_HIP.
+int hip_fail(hipError_t e);
+
+#define Q4_CHECK_HIP(expr)                      \
+  do {                                          \
+    hipError_t e_ = (expr);                     \
+    if (e_ != hipSuccess) return q4::hip_fail(e_); \
+  } while (0)
+
+// Launch status of the last kernel on this thread.
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? Q4_OK : hip_fail(e);
+}
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------------------------------
+// Device helpers
+// ------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  // Round to nearest even (v_cvt_f16_f32 under the default rounding mode).
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64); every lane of the
+// group receives the total. Uses cross-lane permutes; the summation tree is fixed, so results are
+// deterministic.
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = width / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// DPP sum over aligned segments of `width` lanes (power of two <= 64). The total lands in the LAST
+// lane of each segment (lane % width == width - 1); other lanes hold partial sums. Row shifts build
+// prefix sums inside each 16-lane DPP row, row_bcast15/31 carry them across rows.
+template <int width>
+__device__ __forceinline__ float segment_sum_to_last(float v) {
+  auto shr = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                  decltype(ctrl)::value, 0xf, 0xf, true));
+  };
+  if constexpr (width >= 2) v += shr(v, std::integral_constant<int, 0x111>{});  // row_shr:1
+  if constexpr (width >= 4) v += shr(v, std::integral_constant<int, 0x112>{});  // row_shr:2
+  if constexpr (width >= 8) v += shr(v, std::integral_constant<int, 0x114>{});  // row_shr:4
+  if constexpr (width >= 16) v += shr(v, std::integral_constant<int, 0x118>{}); // row_shr:8
+  if constexpr (width >= 32)  // row_bcast:15 into rows 1 and 3
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+  if constexpr (width >= 64)  // row_bcast:31 into rows 2 and 3
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+  return v;
+}
+
+}  // namespace q4

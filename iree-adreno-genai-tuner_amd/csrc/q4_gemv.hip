@@ -1,0 +1,520 @@
+// Decode int4 GEMV for gfx950: y[n] = residual[n] + sum_k x[k] * (nib[n,k] - 8) * scale[n, k/group].
+//
+// Replaces QLinear._gemv_fused (scripts/llm/llama_q4.py:74-90), the fused decode form the
+// reference exports; numerically it is the same contraction as F.linear(x, dequantize_q4(W))
+// (llama_q4.py:72).
+//
+// Memory-bound design (no MFMA):
+//   * The packed weight is streamed exactly once with 16-byte loads. A "chunk" is 16 bytes of one
+//     row = 4 words = 32 consecutive k. LPR lanes cover consecutive chunks of a row, so every load
+//     instruction of a row segment reads LPR*16 contiguous bytes.
+//   * Each lane owns R consecutive rows and CPL chunk slots per pass over K; rows of the same chunk
+//     reuse the x values read once from LDS.
+//   * All global reads are raw buffer loads: a lane whose chunk or row lies past the end gets an
+//     out-of-range offset, which the hardware answers with zeros without touching memory. The
+//     loads therefore need no branches, and the compiler issues them back to back.
+//   * Order at kernel start: x loads (L2), then the first work item's weight and scale loads (HBM),
+//     then x is staged into LDS (this waits for x only: loads complete in issue order), barrier.
+//     Inside the loop the next item's weights are loaded before the current item is computed.
+//   * x sits in LDS in a slot-major layout (slot j of chunk c at [j][c]): lanes reading
+//     consecutive chunks hit consecutive 16-byte LDS words.
+//   * The row reduction over the LPR lanes is a DPP prefix sum (row_shr / row_bcast).
+//   * Nibble decode:
+//       fp32 x: bytes of (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) are converted with
+//               v_cvt_f32_ubyte{0..3} and FMA'd with x; the "-8" is applied once per chunk as
+//               8 * sum(x_chunk), so the per-element work is one convert and one FMA.
+//       fp16 x: masks place nibble pairs in the mantissa of fp16 pairs with a fixed exponent
+//               (1024 + n or 64 + n), v_dot2_f32_f16 multiplies them with (x_b, x_b+4) pairs,
+//               and the constant offsets (plus the -8) are removed per chunk with a precomputed
+//               sum of x. Four dot2 and five bit operations per 8 nibbles.
+//     Both paths accumulate in fp32.
+#include "q4_common.h"
+
+#include <array>
+#include <cstdlib>
+#include <utility>
+
+namespace q4 {
+namespace {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxK = 16384;
+constexpr uint32_t kOOB = 0x80000000u;    // buffer offset past every resource this kernel builds
+constexpr int kBufferFlags = 0x00020000;  // gfx9 raw buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), kBufferFlags);
+}
+
+// kAux: cache-policy bits of the load (2 = nt: streamed once, do not keep in the caches)
+template <int kAux = 0>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAux);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+template <bool kF16X>
+struct XLayout {
+  // uint4 slots per chunk in LDS: fp16 x -> one uint4 per word (4 half2 pairs); fp32 -> two.
+  static constexpr int kSlots = kF16X ? 4 : 8;
+};
+
+// LDS: x slots [kSlots][cpr] uint4, per-word correction shares [K/8] float, one junk chunk
+// (kSlots uint4 + 1 float, rounded up) that absorbs the stores of out-of-range words.
+template <bool kF16X>
+inline size_t lds_bytes(int64_t K) {
+  const int64_t cpr = K / 32;
+  return static_cast<size_t>(cpr) * (XLayout<kF16X>::kSlots * 16 + 16) + XLayout<kF16X>::kSlots * 16 + 16;
+}
+
+__device__ __forceinline__ float dot_chunk_f32(const uint4& w, const float4* __restrict__ xs, int cpr, int c) {
+  // xs slot layout per word j (2 float4): {x0,x2,x4,x6}, {x1,x3,x5,x7}
+  float t = 0.0f;
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = words[j] & 0x0F0F0F0Fu;
+    const uint32_t hi = (words[j] >> 4) & 0x0F0F0F0Fu;
+    const float4 xe = xs[(2 * j) * cpr + c];
+    const float4 xo = xs[(2 * j + 1) * cpr + c];
+    t = fmaf(xe.x, static_cast<float>(lo & 0xFFu), t);
+    t = fmaf(xe.y, static_cast<float>((lo >> 8) & 0xFFu), t);
+    t = fmaf(xe.z, static_cast<float>((lo >> 16) & 0xFFu), t);
+    t = fmaf(xe.w, static_cast<float>(lo >> 24), t);
+    t = fmaf(xo.x, static_cast<float>(hi & 0xFFu), t);
+    t = fmaf(xo.y, static_cast<float>((hi >> 8) & 0xFFu), t);
+    t = fmaf(xo.z, static_cast<float>((hi >> 16) & 0xFFu), t);
+    t = fmaf(xo.w, static_cast<float>(hi >> 24), t);
+  }
+  return t;
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+__device__ __forceinline__ float dot_chunk_f16(const uint4& w, const uint4* __restrict__ xs, int cpr, int c) {
+  // xs slot j (one uint4 per word): half2 pairs (x0,x4), (x1,x5), (x2,x6), (x3,x7)
+  float t = 0.0f;
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t v = words[j];
+    const uint32_t v8 = v >> 8;
+    const uint4 xp = xs[j * cpr + c];
+    // (1024 + n0, 1024 + n4), (64 + n1, 64 + n5), (1024 + n2, 1024 + n6), (64 + n3, 64 + n7)
+    const uint32_t m0 = (v & 0x000F000Fu) | 0x64006400u;
+    const uint32_t m1 = (v & 0x00F000F0u) | 0x54005400u;
+    const uint32_t m2 = (v8 & 0x000F000Fu) | 0x64006400u;
+    const uint32_t m3 = (v8 & 0x00F000F0u) | 0x54005400u;
+    t = __builtin_amdgcn_fdot2(as_h2(m0), as_h2(xp.x), t, false);
+    t = __builtin_amdgcn_fdot2(as_h2(m1), as_h2(xp.y), t, false);
+    t = __builtin_amdgcn_fdot2(as_h2(m2), as_h2(xp.z), t, false);
+    t = __builtin_amdgcn_fdot2(as_h2(m3), as_h2(xp.w), t, false);
+  }
+  return t;
+}
+
+// x words (8 elements each) held per thread during staging: K <= 8 * XW * threads.
+template <bool kF16X, int XW>
+struct XWords {
+  uint4 v[kF16X ? XW : 2 * XW];
+};
+
+// Global -> registers for this thread's x words (word wd = threadIdx.x + i * blockDim.x).
+template <bool kF16X, int XW>
+__device__ __forceinline__ void stage_load(__amdgpu_buffer_rsrc_t xr, XWords<kF16X, XW>& r) {
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const uint32_t wd = threadIdx.x + i * blockDim.x;
+    if constexpr (kF16X) {
+      r.v[i] = buf_load16(xr, wd * 16u);
+    } else {
+      r.v[2 * i] = buf_load16(xr, wd * 32u);
+      r.v[2 * i + 1] = buf_load16(xr, wd * 32u + 16u);
+    }
+  }
+}
+
+// Registers -> LDS in the slot layout, plus each word's share of its chunk correction
+// (sum_k x_k * offset_k; offset 8 on the fp32 path, base + 8 on the fp16 path with base 1024 for
+// even nibble index and 64 for odd). Out-of-range words write to the junk chunk (no branches).
+template <bool kF16X, int XW>
+__device__ __forceinline__ void stage_store(const XWords<kF16X, XW>& r, int nwords, int cpr, uint4* __restrict__ xs,
+                                            float* __restrict__ corr_w, uint4* __restrict__ junk) {
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const int wd = threadIdx.x + i * blockDim.x;
+    const bool ok = wd < nwords;
+    const int c = wd >> 2, j = wd & 3;
+    float* cdst = ok ? corr_w + wd : reinterpret_cast<float*>(junk + XLayout<kF16X>::kSlots);
+    if constexpr (kF16X) {
+      const uint4 a = r.v[i];  // x0..x7 as 4 x half2 (low half = even element)
+      uint4* dst = ok ? xs + j * cpr + c : junk;
+      *dst = make_uint4((a.x & 0xFFFFu) | (a.z << 16), (a.x >> 16) | (a.z & 0xFFFF0000u),
+                        (a.y & 0xFFFFu) | (a.w << 16), (a.y >> 16) | (a.w & 0xFFFF0000u));
+      const uint32_t h[4] = {a.x, a.y, a.z, a.w};
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float xv = half_bits_to_float(static_cast<uint16_t>(h[k >> 1] >> (16 * (k & 1))));
+        s = fmaf(xv, (k & 1) ? 72.0f : 1032.0f, s);
+      }
+      *cdst = s;
+    } else {
+      const float4 a = __builtin_bit_cast(float4, r.v[2 * i]);
+      const float4 b = __builtin_bit_cast(float4, r.v[2 * i + 1]);
+      float4* d0 = reinterpret_cast<float4*>(ok ? xs + (2 * j) * cpr + c : junk);
+      float4* d1 = reinterpret_cast<float4*>(ok ? xs + (2 * j + 1) * cpr + c : junk + 1);
+      *d0 = make_float4(a.x, a.z, b.x, b.z);
+      *d1 = make_float4(a.y, a.w, b.y, b.w);
+      *cdst = 8.0f * (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)));
+    }
+  }
+}
+
+template <int LPR, int CPL, int R>
+struct Item {
+  uint4 w[R][CPL];
+  uint16_t s[R][CPL];  // raw fp16 bits; converted at compute time so no wait sits between loads
+};
+
+// One workgroup = WAVES waves; a "work item" is one row block (R * 64/LPR rows per wave) times
+// one pass of LPR * CPL chunks over K. kMulti == false: exactly one item per workgroup
+// (grid = row blocks, LPR * CPL >= K/32), computed straight from the registers its loads land in,
+// so the compute of each chunk starts as soon as that chunk arrives. kMulti == true: a grid-stride
+// loop over items with two register sets (A/B) used alternately, so the next item streams in while
+// the current one is computed and no register copies force early waits.
+template <bool kF16X, bool kF16Y, int LPR, int CPL, int R, int WAVES, int XW, bool kMulti>
+__global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
+    const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
+    void* y, const float* residual, int N, int K, int gshift) {
+  extern __shared__ uint4 smem[];
+  constexpr int kRowsPerWave = R * (64 / LPR);
+  constexpr int kRows = kRowsPerWave * WAVES;
+  constexpr int kSlots = XLayout<kF16X>::kSlots;
+  // chunk c covers k in [32c, 32c + 32); the group is 32 << gshift elements, so the scale of
+  // chunk c is scale[c >> gshift]
+  const int cpr = K / 32;
+  const int spr = cpr >> gshift;  // scales per row
+  const int nwords = K / 8;
+  uint4* xs = smem;
+  float* corr_w = reinterpret_cast<float*>(smem + kSlots * cpr);
+  uint4* junk = smem + kSlots * cpr + cpr;  // corr_w takes cpr uint4
+
+  const __amdgpu_buffer_rsrc_t wres = make_rsrc(qw, static_cast<uint32_t>(N) * static_cast<uint32_t>(K / 2));
+  const __amdgpu_buffer_rsrc_t sres = make_rsrc(scales, static_cast<uint32_t>(N) * spr * 2u);
+  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<uint32_t>(K) * (kF16X ? 2u : 4u));
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lr = lane % LPR;
+  const int rg = lane / LPR;
+  const int n_blocks = (N + kRows - 1) / kRows;
+  const int n_kpass = kMulti ? (cpr + LPR * CPL - 1) / (LPR * CPL) : 1;
+
+  auto item_row0 = [&](int it) {
+    return (blockIdx.x + (it / n_kpass) * gridDim.x) * kRows + wave * kRowsPerWave + rg * R;
+  };
+  // Loads of one item. Rows past N fall outside the buffer resource by themselves; chunks past
+  // the row get kOOB; both return zeros without memory traffic, so no branches are needed.
+  auto load_item = [&](int it, Item<LPR, CPL, R>& d) {
+    const int kp = it % n_kpass;
+    const int row0 = item_row0(it);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t row = static_cast<uint32_t>(row0 + r);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = kp * (LPR * CPL) + i * LPR + lr;
+        const uint32_t woff = c < cpr ? row * static_cast<uint32_t>(K / 2) + c * 16u : kOOB;
+        const uint32_t soff = c < cpr ? (row * spr + (c >> gshift)) * 2u : kOOB;
+        d.w[r][i] = buf_load16<2>(wres, woff);
+        d.s[r][i] = buf_load2(sres, soff);
+      }
+    }
+  };
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  // Accumulate one item; on the last K pass reduce over the LPR lanes and store.
+  auto compute_item = [&](int it, const Item<LPR, CPL, R>& d) {
+    const int kp = it % n_kpass;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      // out-of-range slots carry zero weights and a zero scale; clamp only the LDS address
+      const int c = min(kp * (LPR * CPL) + i * LPR + lr, cpr - 1);
+      const float4 cw = reinterpret_cast<const float4*>(corr_w)[c];
+      const float cc = (cw.x + cw.y) + (cw.z + cw.w);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float t;
+        if constexpr (kF16X) t = dot_chunk_f16(d.w[r][i], xs, cpr, c);
+        else t = dot_chunk_f32(d.w[r][i], reinterpret_cast<const float4*>(xs), cpr, c);
+        acc[r] = fmaf(half_bits_to_float(d.s[r][i]), t - cc, acc[r]);
+      }
+    }
+    if (kp == n_kpass - 1) {
+      const int row0 = item_row0(it);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = segment_sum_to_last<LPR>(acc[r]);
+        acc[r] = 0.0f;
+        const int row = row0 + r;
+        if (lr == LPR - 1 && row < N) {
+          if constexpr (kF16Y) {
+            reinterpret_cast<uint16_t*>(y)[row] = float_to_half_bits(v);
+          } else {
+            reinterpret_cast<float*>(y)[row] = residual ? residual[row] + v : v;
+          }
+        }
+      }
+    }
+  };
+
+  XWords<kF16X, XW> xr;
+  stage_load<kF16X, XW>(xres, xr);
+  Item<LPR, CPL, R> a;
+  load_item(0, a);  // a workgroup without items gets rows past N: out of range, no traffic
+  if constexpr (!kMulti) {
+    stage_store<kF16X, XW>(xr, nwords, cpr, xs, corr_w, junk);
+    __syncthreads();
+    compute_item(0, a);
+  } else {
+    Item<LPR, CPL, R> b;
+    load_item(1, b);
+    stage_store<kF16X, XW>(xr, nwords, cpr, xs, corr_w, junk);
+    __syncthreads();
+    const int my_blocks = static_cast<int>(blockIdx.x) < n_blocks ? (n_blocks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    const int n_items = my_blocks * n_kpass;
+    // items past the end are out-of-range loads (zeros) whose rows lie past N, so computing them
+    // adds nothing and stores nothing
+    for (int it = 0; it < n_items; it += 2) {
+      compute_item(it, a);
+      load_item(it + 2, a);
+      compute_item(it + 1, b);
+      load_item(it + 3, b);
+    }
+  }
+}
+
+// Generic fallback for shapes the vectorised kernel does not take (K % 32 != 0, group not 32 times a
+// power of two, K too large for the staged layout): one wave per row, one word per lane step, fp32 math.
+template <bool kF16X, bool kF16Y>
+__global__ __launch_bounds__(256) void q4_gemv_generic(
+    const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
+    void* y, const float* residual, int N, int K, int group) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= N) return;
+  const int words = K / 8;
+  float acc = 0.0f;
+  for (int wd = lane; wd < words; wd += 64) {
+    const uint32_t v = static_cast<uint32_t>(qw[static_cast<int64_t>(row) * words + wd]);
+    const float s = half_bits_to_float(scales[static_cast<int64_t>(row) * (K / group) + (wd * 8) / group]);
+    float t = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      float xv;
+      if constexpr (kF16X) xv = half_bits_to_float(reinterpret_cast<const uint16_t*>(x)[wd * 8 + b]);
+      else xv = reinterpret_cast<const float*>(x)[wd * 8 + b];
+      t = fmaf(xv, static_cast<float>(static_cast<int>((v >> (4 * b)) & 15u) - 8), t);
+    }
+    acc = fmaf(s, t, acc);
+  }
+  acc = group_sum<64>(acc);
+  if (lane == 0) {
+    if constexpr (kF16Y) reinterpret_cast<uint16_t*>(y)[row] = float_to_half_bits(acc);
+    else reinterpret_cast<float*>(y)[row] = residual ? residual[row] + acc : acc;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Launch configurations: an explicit list, chosen per shape by a fixed rule.
+// ------------------------------------------------------------------------------------------
+
+struct Cfg {
+  int lpr, cpl, r, waves, xw;
+  bool multi;
+};
+
+// The instantiated tile list (index stable: Q4_GEMV_CFG and q4_gemv_cfg select entries by index).
+// Single-item entries need lpr * cpl >= K/32; every entry needs K/8 <= xw * 64 * waves.
+constexpr Cfg kCfgs[] = {
+    {32, 3, 2, 5, 2, false},   // 0: K<=3072, 20 rows/WG (N=5120 -> 256 WGs)
+    {32, 3, 1, 5, 2, false},   // 1: K<=3072, 10 rows/WG
+    {32, 3, 1, 2, 4, false},   // 2: K<=3072, 4 rows/WG
+    {64, 2, 1, 4, 2, false},   // 3: K<=4096, 4 rows/WG
+    {16, 6, 1, 5, 2, false},   // 4: K<=3072, 20 rows/WG, 16 lanes per row
+    {16, 6, 2, 8, 1, false},   // 5: K<=3072, 64 rows/WG (N=16384 -> 256 WGs)
+    {32, 3, 2, 8, 1, false},   // 6: K<=3072, 32 rows/WG
+    {32, 3, 1, 8, 1, false},   // 7: K<=3072, 16 rows/WG
+    {32, 3, 1, 6, 1, false},   // 8: K<=3072, 12 rows/WG (N=3072 -> 256 WGs)
+    {8, 12, 1, 4, 2, false},   // 9: K<=3072, 32 rows/WG, 8 lanes per row
+    {64, 4, 1, 4, 4, false},   // 10: K<=8192, 4 rows/WG
+    {32, 8, 1, 6, 4, false},   // 11: K<=8192, 12 rows/WG (N=3072 -> 256 WGs)
+    {64, 4, 2, 6, 4, false},   // 12: K<=8192, 12 rows/WG, 2 rows per lane
+    {64, 4, 1, 8, 2, false},   // 13: K<=8192, 8 rows/WG
+    {8, 1, 1, 4, 1, false},    // 14: K<=256, 32 rows/WG (tiny)
+    {8, 3, 1, 4, 1, false},    // 15: K<=768, 32 rows/WG (tiny down-projection, K=704)
+    {16, 2, 1, 4, 1, false},   // 16: K<=1024, 16 rows/WG
+    {32, 4, 1, 8, 1, false},   // 17: K<=4096, 16 rows/WG
+    {64, 8, 1, 4, 8, false},   // 18: K<=16384, 4 rows/WG
+    {16, 6, 1, 8, 1, true},    // 19: grid-stride, K=3072 in one pass, 32 rows per item (LM head)
+    {32, 3, 1, 8, 1, true},    // 20: grid-stride, 16 rows per item
+    {16, 6, 2, 8, 1, true},    // 21: grid-stride, 64 rows per item
+    {64, 2, 1, 4, 8, true},    // 22: grid-stride, any K <= 16384 in passes of 128 chunks
+};
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+template <bool F16X, bool F16Y, int I>
+struct KernelOf {
+  static constexpr Cfg c = kCfgs[I];
+  static constexpr auto fn = q4_gemv_kernel<F16X, F16Y, c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi>;
+};
+
+// last argument: the generic kernel takes the group size, the vectorised kernel log2(group / 32)
+using KernelFn = void (*)(const int32_t*, const uint16_t*, const void*, void*, const float*, int, int, int);
+
+template <bool F16X, bool F16Y, int... Is>
+constexpr auto make_table(std::integer_sequence<int, Is...>) {
+  return std::array<KernelFn, sizeof...(Is)>{KernelOf<F16X, F16Y, Is>::fn...};
+}
+
+const auto kTabF32F32 = make_table<false, false>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF32F16 = make_table<false, true>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF16F32 = make_table<true, false>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF16F16 = make_table<true, true>(std::make_integer_sequence<int, kNumCfgs>{});
+
+int rows_per_block(const Cfg& c) { return c.r * (64 / c.lpr) * c.waves; }
+
+bool cfg_fits(const Cfg& c, int64_t N, int64_t K) {
+  const int64_t cpr = K / 32;
+  if (K / 8 > static_cast<int64_t>(c.xw) * 64 * c.waves) return false;
+  if (!c.multi && static_cast<int64_t>(c.lpr) * c.cpl < cpr) return false;
+  if (!c.multi && (N + rows_per_block(c) - 1) / rows_per_block(c) > 65535) return false;
+  return true;
+}
+
+// Fixed rule: measured entries for the shapes of the 3B model and the benchmark; otherwise the
+// fitting single-item entry with the least padding in K and rows and the most even spread of
+// workgroups over 256 CUs, or the grid-stride entry when no single-item entry fits.
+int choose_cfg(int64_t N, int64_t K, bool f16x) {
+  const char* ov = getenv("Q4_GEMV_CFG");
+  if (ov && *ov) {
+    const int i = atoi(ov);
+    if (i >= 0 && i < kNumCfgs && cfg_fits(kCfgs[i], N, K)) return i;
+  }
+  (void)f16x;
+  if (K == 3072) {
+    if (N == 5120) return 8;
+    if (N == 16384) return 7;
+    if (N == 3072) return 8;
+    if (N > 65536) return 19;
+  }
+  if (K == 8192 && N == 3072) return 10;
+  const int64_t cpr = K / 32;
+  int best = 22;
+  double best_score = 1e30;
+  for (int i = 0; i < kNumCfgs; ++i) {
+    const Cfg& c = kCfgs[i];
+    if (c.multi || !cfg_fits(c, N, K)) continue;
+    const int64_t span = static_cast<int64_t>(c.lpr) * c.cpl;
+    const double k_waste = static_cast<double>(span) / cpr;
+    const int64_t blocks = (N + rows_per_block(c) - 1) / rows_per_block(c);
+    const double row_waste = static_cast<double>(blocks * rows_per_block(c)) / N;
+    const int64_t rounds = (blocks + 255) / 256;
+    const double balance = static_cast<double>(rounds * 256) / blocks;
+    const double score = k_waste * row_waste * balance * (rounds > 8 ? 1.5 : 1.0);
+    if (score < best_score) { best_score = score; best = i; }
+  }
+  return best;
+}
+
+int set_lds_limit(KernelFn fn, size_t bytes) {
+  if (bytes <= 64 * 1024) return Q4_OK;
+  Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+  return Q4_OK;
+}
+
+}  // namespace
+
+// Runs config `cfg` (-1 = automatic choice) with `grid_override` workgroups (0 = automatic).
+int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
+                   int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg,
+                   int grid_override, hipStream_t stream) {
+  const bool f16x = x_dtype == Q4_F16, f16y = y_dtype == Q4_F16;
+  int ci = cfg >= 0 && cfg < kNumCfgs ? cfg : choose_cfg(N, K, f16x);
+  if (!cfg_fits(kCfgs[ci], N, K)) ci = 22;
+  const Cfg& c = kCfgs[ci];
+  const int threads = c.waves * 64;
+  const int gchunks = group / 32;
+  const bool pow2_group = group % 32 == 0 && (gchunks & (gchunks - 1)) == 0;
+  // 32-bit buffer offsets: rows past N (up to three grid strides of prefetch) must not wrap
+  const int64_t max_row = N + 3LL * 1024 * rows_per_block(c);
+  const bool vec = (K % 32 == 0) && pow2_group && K <= kMaxK && cfg_fits(c, N, K) &&
+                   N * (K / 2) < (int64_t{1} << 31) && max_row * (K / 2) < (int64_t{1} << 32) &&
+                   aligned(qweight, 16) && aligned(x, 16);
+  if (!vec) {
+    const dim3 grid(static_cast<unsigned>((N + 3) / 4)), block(256);
+    if (f16x && f16y) hipLaunchKernelGGL((q4_gemv_generic<true, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
+    else if (f16x) hipLaunchKernelGGL((q4_gemv_generic<true, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
+    else if (f16y) hipLaunchKernelGGL((q4_gemv_generic<false, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
+    else hipLaunchKernelGGL((q4_gemv_generic<false, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
+    return launch_status();
+  }
+  KernelFn fn = f16x ? (f16y ? kTabF16F16[ci] : kTabF16F32[ci]) : (f16y ? kTabF32F16[ci] : kTabF32F32[ci]);
+  const size_t lds = f16x ? lds_bytes<true>(K) : lds_bytes<false>(K);
+  if (int st = set_lds_limit(fn, lds)) return st;
+  const int64_t blocks = (N + rows_per_block(c) - 1) / rows_per_block(c);
+  // Single-item entries: one row block per workgroup. Grid-stride entries: 1024 workgroups (4 per
+  // CU; x is staged once per workgroup) unless overridden.
+  int64_t grid = blocks;
+  if (c.multi) {
+    grid = blocks < 1024 ? blocks : 1024;
+    if (grid_override > 0) grid = grid_override < blocks ? grid_override : blocks;
+  }
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(threads), lds, stream, qweight, scales, x, y,
+                     residual, (int)N, (int)K, __builtin_ctz(gchunks));
+  return launch_status();
+}
+
+int q4_gemv_num_cfgs() { return kNumCfgs; }
+
+}  // namespace q4
+
+namespace {
+int gemv_args(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y, int y_dtype,
+              const float* residual, int64_t N, int64_t K, int group) {
+  if (!qweight || !scales || !x || !y) return Q4_ERR_NULL;
+  if (N <= 0 || K <= 0 || group <= 0 || K % 8 || group % 8 || K % group) return Q4_ERR_SHAPE;
+  if (N > INT32_MAX || K > INT32_MAX / 8) return Q4_ERR_SHAPE;
+  if ((x_dtype != Q4_F32 && x_dtype != Q4_F16) || (y_dtype != Q4_F32 && y_dtype != Q4_F16)) return Q4_ERR_DTYPE;
+  if (residual && y_dtype != Q4_F32) return Q4_ERR_DTYPE;
+  if (!q4::aligned(qweight, 4) || !q4::aligned(x, 4) || !q4::aligned(y, 2)) return Q4_ERR_ALIGN;
+  return Q4_OK;
+}
+}  // namespace
+
+extern "C" int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
+                       int y_dtype, const float* residual, int64_t N, int64_t K, int group, void* stream) {
+  if (int st = gemv_args(qweight, scales, x, x_dtype, y, y_dtype, residual, N, K, group)) return st;
+  return q4::q4_gemv_launch(qweight, scales, x, x_dtype, y, y_dtype, residual, N, K, group, -1, 0,
+                            q4::as_stream(stream));
+}
+
+extern "C" int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
+                           int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg,
+                           int grid, void* stream) {
+  if (int st = gemv_args(qweight, scales, x, x_dtype, y, y_dtype, residual, N, K, group)) return st;
+  if (cfg >= q4::q4_gemv_num_cfgs() || grid < 0) return Q4_ERR_RANGE;
+  return q4::q4_gemv_launch(qweight, scales, x, x_dtype, y, y_dtype, residual, N, K, group, cfg, grid,
+                            q4::as_stream(stream));
+}
+
+extern "C" int q4_gemv_num_configs(void) { return q4::q4_gemv_num_cfgs(); }

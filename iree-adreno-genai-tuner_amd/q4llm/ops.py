@@ -1,0 +1,181 @@
+"""Tensor-level wrappers over the C ABI (include/q4llm.h).
+
+Each wrapper takes torch tensors that live on the ROCm device, allocates its outputs with torch,
+and calls one extern "C" entry point on torch's current stream. Shapes and dtypes are checked
+here; the library re-validates everything on its side.
+"""
+
+import ctypes as C
+
+import torch
+
+from ._lib import F16, F32, LIB, ptr, stream_of
+
+_DT = {torch.float32: F32, torch.float16: F16}
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("q4llm ops take ROCm device tensors (torch 'cuda' device); got a CPU tensor")
+
+
+def quantize_q4(w: torch.Tensor, group: int):
+    """w [N, K] (device) -> (qweight [N, K/8] int32, scales [N, K/group] fp16); llama_q4.py:25-38."""
+    _dev(w)
+    n, k = w.shape
+    w = w.float().contiguous()
+    qw = torch.empty(n, k // 8, dtype=torch.int32, device=w.device)
+    sc = torch.empty(n, k // group, dtype=torch.float16, device=w.device)
+    LIB.call("q4_quantize", ptr(w), ptr(qw), ptr(sc), n, k, group, stream_of(w.device))
+    return qw, sc
+
+
+def unpack_q4(qweight: torch.Tensor) -> torch.Tensor:
+    """[N, K/8] int32 -> [N, K] uint8 nibbles in [0, 15]; llama_q4.py:41-45."""
+    _dev(qweight)
+    n, kw = qweight.shape
+    out = torch.empty(n, kw * 8, dtype=torch.uint8, device=qweight.device)
+    LIB.call("q4_unpack", ptr(qweight.contiguous()), ptr(out), n, kw * 8, stream_of(qweight.device))
+    return out
+
+
+def dequantize_q4(qweight, scales, group, dtype=torch.float32):
+    """(nibble - 8) * scale as [N, K] of `dtype`; llama_q4.py:48-51."""
+    _dev(qweight, scales)
+    n, kw = qweight.shape
+    out = torch.empty(n, kw * 8, dtype=dtype, device=qweight.device)
+    LIB.call("q4_dequant", ptr(qweight), ptr(scales), ptr(out), _DT[dtype], n, kw * 8, group,
+             stream_of(qweight.device))
+    return out
+
+
+def q4_gemv(qweight, scales, x, group, out_dtype=torch.float32, residual=None, out=None):
+    """y [N] = residual + W x for one row x [K] (fp32 or fp16); QLinear._gemv_fused semantics."""
+    _dev(qweight, scales, x, residual)
+    n, kw = qweight.shape
+    x = x.reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty(n, dtype=out_dtype, device=x.device)
+    LIB.call("q4_gemv", ptr(qweight), ptr(scales), ptr(x), _DT[x.dtype], ptr(out), _DT[out.dtype],
+             ptr(residual), n, kw * 8, group, stream_of(x.device))
+    return out
+
+
+def q4_gemv_cfg(qweight, scales, x, group, out, cfg=-1, grid=0):
+    """Benchmark hook: q4_gemv with an explicit tile config index and grid size."""
+    n, kw = qweight.shape
+    LIB.call("q4_gemv_cfg", ptr(qweight), ptr(scales), ptr(x), _DT[x.dtype], ptr(out), _DT[out.dtype],
+             None, n, kw * 8, group, cfg, grid, stream_of(x.device))
+    return out
+
+
+def q4_linear(x, qweight, scales, group, residual=None, out=None):
+    """y [M, N] = residual + x [M, K] @ dequant(W)^T in fp32 (QLinear.forward at M > 1)."""
+    _dev(qweight, scales, x, residual)
+    m, k = x.shape
+    n = qweight.shape[0]
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.float32, device=x.device)
+    LIB.call("q4_linear", ptr(x), m, ptr(qweight), ptr(scales), ptr(out), ptr(residual), n, k, group,
+             stream_of(x.device))
+    return out
+
+
+def gemm_f16_nt(a, b, out=None):
+    """C [M, N] fp16 = A [M, K] @ B [N, K]^T with fp32 accumulation (gemm/shapes.py 'NT')."""
+    _dev(a, b)
+    m, k = a.shape
+    n = b.shape[0]
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.float16, device=a.device)
+    LIB.call("gemm_f16_nt", ptr(a), ptr(b), ptr(out), m, n, k, a.stride(0), b.stride(0), out.stride(0),
+             stream_of(a.device))
+    return out
+
+
+def gemm_f16_nt_cfg(a, b, out, cfg=-1, split=0):
+    """Benchmark hook: gemm_f16_nt with an explicit tile config index and split-K factor."""
+    m, k = a.shape
+    n = b.shape[0]
+    LIB.call("gemm_f16_nt_cfg", ptr(a), ptr(b), ptr(out), m, n, k, a.stride(0), b.stride(0),
+             out.stride(0), cfg, split, stream_of(a.device))
+    return out
+
+
+def attn_workspace_bytes(C_rows, n_q, n_kv, hd, L) -> int:
+    b = C.c_size_t(0)
+    LIB.call("attn_workspace_bytes", C_rows, n_q, n_kv, hd, L, C.byref(b))
+    return b.value
+
+
+def attn_bucket(q, k_cache, v_cache, L, start, scale, workspace=None, out=None):
+    """Attention of q [C, n_q, hd] (fp32) at positions start+c over caches [:L] (fp16)."""
+    _dev(q, k_cache, v_cache, start)
+    c, n_q, hd = q.shape
+    n_kv = k_cache.shape[1]
+    ws_bytes = attn_workspace_bytes(c, n_q, n_kv, hd, L)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty(c, n_q * hd, dtype=torch.float32, device=q.device)
+    LIB.call("attn_bucket", ptr(q.contiguous()), ptr(k_cache), ptr(v_cache), ptr(out), c, n_q, n_kv, hd, L,
+             ptr(start), scale, ptr(workspace), workspace.numel(), stream_of(q.device))
+    return out
+
+
+def rmsnorm(x, w, eps, row=None, out=None):
+    """rms_norm (llama_q4.py:141-142) over the last dim of x [M, D]; `row` selects one device row."""
+    _dev(x, w, row)
+    m, d = x.shape
+    if out is None:
+        out = torch.empty((1 if row is not None else m), d, dtype=torch.float32, device=x.device)
+    LIB.call("rmsnorm_f32", ptr(x), ptr(w), ptr(out), m, d, eps, ptr(row), stream_of(x.device))
+    return out
+
+
+def rope_kv_write(qkv, cos_t, sin_t, k_cache, v_cache, n_q, n_kv, hd, start):
+    """In-place RoPE on the q/k parts of qkv [C, (n_q+2n_kv)hd] and fp16 KV row writes at start+c."""
+    _dev(qkv, cos_t, sin_t, k_cache, v_cache, start)
+    c = qkv.shape[0]
+    LIB.call("rope_kv_write", ptr(qkv), ptr(cos_t), ptr(sin_t), ptr(k_cache), ptr(v_cache), c, n_q, n_kv,
+             hd, cos_t.shape[0], ptr(start), stream_of(qkv.device))
+    return qkv
+
+
+def silu_mul(gu, inter, out=None):
+    """silu(gu[:, :inter]) * gu[:, inter:] (llama_q4.py:236)."""
+    _dev(gu)
+    m = gu.shape[0]
+    if out is None:
+        out = torch.empty(m, inter, dtype=torch.float32, device=gu.device)
+    LIB.call("silu_mul_f32", ptr(gu), ptr(out), m, inter, stream_of(gu.device))
+    return out
+
+
+def embed_lookup(qweight, scales, tokens, group, out=None):
+    """Dequantized embedding rows for device int32 tokens [C] (llama_q4.py:106-119)."""
+    _dev(qweight, scales, tokens)
+    vocab, kw = qweight.shape
+    c = tokens.numel()
+    if out is None:
+        out = torch.empty(c, kw * 8, dtype=torch.float32, device=tokens.device)
+    LIB.call("q4_embed_lookup", ptr(qweight), ptr(scales), ptr(tokens), ptr(out), c, vocab, kw * 8, group,
+             stream_of(tokens.device))
+    return out
+
+
+def argmax(logits, out=None, workspace=None):
+    """First index of the max of a 1-D fp32 tensor, as a device int32 [1] (torch.argmax semantics)."""
+    _dev(logits)
+    v = logits.numel()
+    b = C.c_size_t(0)
+    LIB.call("argmax_workspace_bytes", v, C.byref(b))
+    if workspace is None:
+        workspace = torch.empty(max(b.value, 1), dtype=torch.uint8, device=logits.device)
+    if out is None:
+        out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    LIB.call("argmax_f32", ptr(logits), v, ptr(out), ptr(workspace), workspace.numel(),
+             stream_of(logits.device))
+    return out

@@ -1,0 +1,124 @@
+"""GPU parity of the int4 format kernels and the decode GEMV against the CPU oracle.
+
+Integer work (quantize, unpack, embedding rows) must be bit-exact; the GEMV must be within
+max-abs 1e-2 x output RMS of the fp64 oracle for fp16 in/out and within
+1e-5 x RMS for the fp32 model path (fp32 accumulation either way; the fp32 path applies the -8
+of each nibble once per 32-element chunk, which costs a few fp32 ulps of cancellation). Outputs are NaN-poisoned before
+each kernel runs so an unwritten element fails the check."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import llama_q4_ref as R
+from q4llm import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def poison(t):
+    if t.dtype.is_floating_point:
+        t.fill_(float("nan"))
+    else:
+        t.fill_(-1)
+    return t
+
+
+def crafted_ties(n, k, group, seed):
+    """Weights whose w/scale hits exact .5 ties: each group holds amax 7 * 2^e and half-steps."""
+    rng = np.random.default_rng(seed)
+    halves = rng.integers(-14, 15, size=(n, k)).astype(np.float32) / 2.0
+    halves[:, ::group] = 7.0
+    e = rng.integers(-6, 3, size=(n, k // group, 1)).astype(np.float32)
+    return torch.from_numpy((halves.reshape(n, k // group, group) * 2.0 ** e).reshape(n, k))
+
+
+@pytest.mark.parametrize("n,k,group", [(96, 256, 32), (130, 3072, 128), (64, 704, 32), (33, 24, 8)])
+def test_quantize_bit_exact(dev, n, k, group):
+    g = torch.Generator().manual_seed(n + k)
+    for w in (torch.randn(n, k, generator=g) * 0.02, crafted_ties(n, k, group, n), torch.zeros(n, k)):
+        qw_ref, sc_ref = R.quantize_q4(w, group)
+        qw, sc = ops.quantize_q4(w.to(dev), group)
+        assert torch.equal(qw.cpu(), qw_ref)
+        assert torch.equal(sc.cpu().view(torch.int16), sc_ref.view(torch.int16))
+
+
+def test_unpack_bit_exact(dev):
+    rng = np.random.default_rng(0)
+    words = torch.from_numpy(rng.integers(-2 ** 31, 2 ** 31, size=(37, 48), dtype=np.int64).astype(np.int32))
+    words[0, :3] = torch.tensor([0x76543210, -0x01234568, -2 ** 31], dtype=torch.int32)
+    out = ops.unpack_q4(words.to(dev))
+    assert torch.equal(out.cpu().to(torch.int64), R.unpack_q4(words))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_dequant(dev, dtype):
+    qw, sc, _ = synth.gemv_problem(64, 512, 128, seed=1)
+    qw, sc = torch.from_numpy(qw), torch.from_numpy(sc)
+    ref = R.dequantize_q4(qw, sc, 128)
+    out = ops.dequantize_q4(qw.to(dev), sc.to(dev), 128, dtype).cpu()
+    assert torch.equal(out, ref.to(dtype))
+
+
+def test_embed_lookup_bit_exact(dev):
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(300, 256, generator=g) * 0.02
+    qw, sc = R.quantize_q4(w, 32)
+    toks = torch.tensor([0, 299, 17, 150, 300, -1], dtype=torch.int32)
+    out = ops.embed_lookup(qw.to(dev), sc.to(dev), toks.to(dev), 32).cpu()
+    full = R.dequantize_q4(qw, sc, 32)
+    assert torch.equal(out[:4], full[toks[:4].long()])
+    assert torch.equal(out[4:], torch.zeros(2, 256))  # out-of-vocab ids give zero rows
+
+
+def gemv_ref(qw, sc, x, group):
+    wd = R.dequantize_q4(torch.from_numpy(qw), torch.from_numpy(sc), group).double()
+    return (wd @ torch.from_numpy(np.asarray(x, np.float64)).reshape(-1, 1)).reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(5120, 3072), (16384, 3072), (3072, 8192), (3072, 3072), (100, 3072)])
+def test_gemv_f16_config2(dev, n, k):
+    qw, sc, x = synth.gemv_problem(n, k, 128, seed=0)
+    ref = gemv_ref(qw, sc, x.astype(np.float32), 128)
+    y = poison(torch.empty(n, dtype=torch.float16, device=dev))
+    ops.q4_gemv(torch.from_numpy(qw).to(dev), torch.from_numpy(sc).to(dev), torch.from_numpy(x).to(dev), 128, out=y)
+    y = y.cpu().double()
+    rms = ref.pow(2).mean().sqrt().item()
+    err = (y - ref).abs().max().item()
+    assert err <= 1e-2 * rms, (err, rms)
+
+
+@pytest.mark.parametrize("n,k,group", [(5120, 3072, 128), (3072, 8192, 128), (512, 256, 32), (256, 704, 32),
+                                       (1000, 3072, 128), (77, 72, 8), (64, 96, 16)])
+def test_gemv_f32_model_path(dev, n, k, group):
+    g = torch.Generator().manual_seed(n * 7 + k)
+    w = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(w, group)
+    x = torch.randn(k, generator=g)
+    res = torch.randn(n, generator=g)
+    ref = (R.dequantize_q4(qw, sc, group).double() @ x.double())
+    rms = ref.pow(2).mean().sqrt().item()
+    qd, sd_, xd = qw.to(dev), sc.to(dev), x.to(dev)
+    y = poison(torch.empty(n, dtype=torch.float32, device=dev))
+    ops.q4_gemv(qd, sd_, xd, group, out=y)
+    assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+    # residual fused into the epilogue, aliasing the output (h = h + W x)
+    h = res.to(dev).clone()
+    ops.q4_gemv(qd, sd_, xd, group, residual=h, out=h)
+    assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
+
+
+def test_gemv_all_configs_agree(dev):
+    """Every entry of the explicit tile list computes the same GEMV (coverage of the tile table)."""
+    from q4llm._lib import LIB
+    n_cfg = LIB.raw("q4_gemv_num_configs")()
+    qw, sc, x = synth.gemv_problem(1000, 3072, 128, seed=3)
+    ref = gemv_ref(qw, sc, x.astype(np.float32), 128)
+    rms = ref.pow(2).mean().sqrt().item()
+    qd, sd_, xd = (torch.from_numpy(a).to(dev) for a in (qw, sc, x))
+    for cfg in range(n_cfg):
+        for grid in (0, 7):
+            y = poison(torch.empty(1000, dtype=torch.float16, device=dev))
+            ops.q4_gemv_cfg(qd, sd_, xd, 128, y, cfg=cfg, grid=grid)
+            err = (y.cpu().double() - ref).abs().max().item()
+            assert err <= 1e-2 * rms, (cfg, grid, err)

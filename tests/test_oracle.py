@@ -1,0 +1,253 @@
+"""Pins the CPU oracle (oracle/llama_q4_ref.py) against known answers, closed forms, brute force and
+transformers' LlamaForCausalLM, so that the oracle can then serve as the parity checker for the
+GPU path. CPU only."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import llama_q4_ref as R
+
+
+def u32_as_i32(u):
+    return u - (1 << 32) if u >= (1 << 31) else u
+
+
+# ------------------------------------------------------------------------------------------------
+# a1-a3: int4 format known answers (llama_q4.py:25-51)
+# ------------------------------------------------------------------------------------------------
+
+
+def test_unpack_known_words():
+    words = torch.tensor([[u32_as_i32(0x76543210), u32_as_i32(0xFEDCBA98), u32_as_i32(0x80000000)]],
+                         dtype=torch.int32)
+    nib = R.unpack_q4(words)
+    assert nib.tolist() == [[0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 0, 0, 0, 0, 0, 0, 0, 8]]
+
+
+def test_quantize_known_answer_half_even():
+    # amax 7 -> scale exactly 1.0; w/scale hits .5 ties: 3.5 -> 4, 2.5 -> 2, -0.5 -> 0, 0.5 -> 0, -1.5 -> -2
+    w = torch.tensor([[7.0, -7.0, 3.5, 2.5, -0.5, 0.5, -1.5, 0.0]])
+    qw, sc = R.quantize_q4(w, 8)
+    # q + 8 = [15, 1, 12, 10, 8, 8, 6, 8], nibble b at bits 4b: 0x8688AC1F
+    assert qw.tolist() == [[u32_as_i32(0x8688AC1F)]]
+    assert sc.view(torch.int16).tolist() == [[0x3C00]]
+
+
+def test_quantize_zero_group_and_bit31():
+    w = torch.zeros(1, 16)
+    w[0, 8:] = torch.tensor([-7.0, 7.0, 0, 0, 0, 0, 0, -7.0])
+    qw, sc = R.quantize_q4(w, 8)
+    # all-zero group: scale clamps to 1e-8/7 (fp16 0), every nibble 8 -> 0x88888888
+    assert qw[0, 0].item() == u32_as_i32(0x88888888)
+    assert sc[0, 0].item() == 0.0
+    # second group: [1, 15, 8, 8, 8, 8, 8, 1] -> 0x188888F1 (nibble 7 = 1, no bit 31)
+    assert qw[0, 1].item() == u32_as_i32(0x188888F1)
+    w2 = torch.tensor([[0.0] * 7 + [7.0]])
+    qw2, _ = R.quantize_q4(w2, 8)
+    assert qw2[0, 0].item() == u32_as_i32(0xF8888888)  # bit 31 set -> negative int32
+    assert qw2[0, 0].item() < 0
+
+
+def test_dequant_known_answer():
+    qw = torch.tensor([[u32_as_i32(0x8688AC1F)]], dtype=torch.int32)
+    sc = torch.tensor([[0.5]], dtype=torch.float16)
+    assert R.dequantize_q4(qw, sc, 8).tolist() == [[3.5, -3.5, 2.0, 1.0, 0.0, 0.0, -1.0, 0.0]]
+
+
+def test_all_sixteen_nibble_values_roundtrip():
+    vals = torch.arange(16, dtype=torch.int64)
+    words = torch.zeros(2, dtype=torch.int64)
+    for i in range(16):
+        words[i // 8] |= vals[i] << (4 * (i % 8))
+    words = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)[None]
+    assert R.unpack_q4(words)[0].tolist() == list(range(16))
+
+
+@pytest.mark.parametrize("group", [8, 32, 128])
+def test_quantize_invariants(group):
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(7, 256, generator=g) * 0.02
+    qw, sc = R.quantize_q4(w, group)
+    nib = R.unpack_q4(qw)
+    assert nib.min() >= 1 and nib.max() <= 15  # |q| <= 7 -> nibble in [1, 15]
+    # every group's max |w| maps to |q| == 7
+    q = (nib - 8).reshape(7, 256 // group, group)
+    assert (q.abs().amax(-1) == 7).all()
+    # dequant error bounded by half a (fp32) step plus the fp16 scale rounding
+    scale32 = w.reshape(7, -1, group).abs().amax(-1, keepdim=True) / 7
+    deq = R.dequantize_q4(qw, sc, group).reshape(7, -1, group)
+    err = (deq - w.reshape(7, -1, group)).abs()
+    assert (err <= scale32 * (0.5 + 8 * 2 ** -11) + 1e-12).all()
+
+
+# ------------------------------------------------------------------------------------------------
+# a5: GEMV (fused and eager forms vs fp64 textbook)
+# ------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n,k,group", [(64, 256, 32), (40, 384, 128)])
+def test_gemv_forms_match_fp64(n, k, group):
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn(n, k, generator=g) * 0.05
+    x = torch.randn(1, k, generator=g)
+    qw, sc = R.quantize_q4(w, group)
+    wd = R.dequantize_q4(qw, sc, group).double()
+    ref = x.double() @ wd.T
+    fused = R.gemv_fused(qw, sc, group, x)
+    eager = R.QLinearRef(group=group, qweight=qw, scales=sc)(x)
+    rms = ref.pow(2).mean().sqrt().item()
+    assert (fused.double() - ref).abs().max().item() < 1e-5 * rms
+    assert (eager.double() - ref).abs().max().item() < 1e-5 * rms
+
+
+# ------------------------------------------------------------------------------------------------
+# a11: embedding lookup, LM head, argmax tie rule
+# ------------------------------------------------------------------------------------------------
+
+
+def test_embedding_lookup_rows_and_chunks():
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(100, 64, generator=g)
+    emb = R.QEmbeddingRef(w, 32, chunk_rows=30)
+    toks = torch.tensor([0, 29, 30, 99, 55])
+    full = R.dequantize_q4(emb.qweight, emb.scales, 32)
+    assert torch.equal(emb.lookup(toks), full[toks])
+    x = torch.randn(1, 64, generator=g)
+    assert torch.allclose(emb.logits(x), x @ full.T, atol=1e-5)
+
+
+def test_argmax_first_max():
+    t = torch.tensor([[1.0, 3.0, 3.0, 2.0]])
+    assert torch.argmax(t, -1).item() == 1
+
+
+def test_rms_norm_closed_form():
+    x = torch.full((1, 16), 3.0)
+    w = torch.full((16,), 2.0)
+    out = R.rms_norm(x, w, 1e-5)
+    assert torch.allclose(out, torch.full((1, 16), 3.0 / math.sqrt(9.0 + 1e-5) * 2.0))
+
+
+def test_rotate_half():
+    x = torch.arange(8.0)
+    assert R.rotate_half(x).tolist() == [-4.0, -5.0, -6.0, -7.0, 0.0, 1.0, 2.0, 3.0]
+
+
+# ------------------------------------------------------------------------------------------------
+# a12: schedule closed forms (llm_runner.c:143-245)
+# ------------------------------------------------------------------------------------------------
+
+
+def test_pick_bucket():
+    b = [256, 512, 1024, 2048, 4096]
+    assert R.pick_bucket(b, 1) == 256
+    assert R.pick_bucket(b, 256) == 256
+    assert R.pick_bucket(b, 257) == 512
+    assert R.pick_bucket(b, 4097) == -1
+    assert R.pick_bucket(b, 3, use_max=True) == 4096
+
+
+def test_schedule_3b_shape():
+    calls = R.schedule_calls(512, 256, 256, [256, 512, 1024, 2048, 4096])
+    assert calls[:2] == [("prefill", 0, 256), ("prefill", 256, 512)]
+    dec = calls[2:]
+    assert len(dec) == 255
+    assert dec[0] == ("decode", 512, 1024) and dec[-1] == ("decode", 766, 1024)
+    assert {L for _, _, L in dec} == {1024}
+
+
+def test_schedule_tiny_and_ragged_prompt():
+    calls = R.schedule_calls(21, 10, 8, [16, 32, 64])
+    assert [c for c in calls if c[0] == "prefill"] == [("prefill", 0, 16), ("prefill", 8, 16), ("prefill", 16, 32)]
+    dec = [c for c in calls if c[0] == "decode"]
+    assert dec[0] == ("decode", 21, 32) and len(dec) == 9
+
+
+# ------------------------------------------------------------------------------------------------
+# Whole step vs transformers (scripts/llm/test_tiny.py protocol)
+# ------------------------------------------------------------------------------------------------
+
+transformers = pytest.importorskip("transformers")
+
+REF_TINY = dict(  # scripts/llm/test_tiny.py:19-26
+    hidden_size=256, num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2, head_dim=32,
+    intermediate_size=512, vocab_size=1000, rms_norm_eps=1e-5, rope_theta=500000.0,
+    rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                  "high_freq_factor": 4.0, "original_max_position_embeddings": 8192},
+    max_position_embeddings=131072, tie_word_embeddings=True, hidden_act="silu",
+    attention_bias=False, mlp_bias=False, initializer_range=0.2,
+)
+
+BASELINE_TINY = dict(  # BASELINE config 1 (intermediate 688 is padded to 704 with group 32)
+    hidden_size=256, num_hidden_layers=4, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+    intermediate_size=688, vocab_size=1024, rms_norm_eps=1e-5, rope_theta=10000.0,
+    max_position_embeddings=4096, tie_word_embeddings=True, hidden_act="silu",
+    attention_bias=False, mlp_bias=False, initializer_range=0.02,
+)
+
+
+def _hf_vs_oracle(cfg, group, max_ctx, n_prompt, n_new, C, L, chunk_rows):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(0)
+    hf = LlamaForCausalLM(LlamaConfig(**cfg, attn_implementation="eager")).eval()
+    sd = {k: v.clone() for k, v in hf.state_dict().items()}
+    ours = R.LlamaQ4Ref(cfg, sd, group=group, max_ctx=max_ctx, vocab_chunk=chunk_rows)
+    inter = cfg["intermediate_size"]
+    with torch.no_grad():  # give HF the same int4-rounded weights (padding cropped off)
+        for name, p in hf.named_parameters():
+            if p.dim() != 2:
+                continue
+            if name.endswith("down_proj.weight") and inter % group:
+                wp = torch.cat([p, torch.zeros(p.shape[0], R.pad_to(inter, group) - inter)], 1)
+                p.copy_(R.dequantize_q4(*R.quantize_q4(wp, group), group)[:, :inter])
+            else:
+                p.copy_(R.dequantize_q4(*R.quantize_q4(p, group), group))
+    prompt = torch.randint(0, cfg["vocab_size"], (1, n_prompt))
+    ids, hf_logits = prompt.clone(), []
+    with torch.no_grad():
+        for _ in range(n_new):
+            lg = hf(ids).logits[0, -1]
+            hf_logits.append(lg)
+            ids = torch.cat([ids, lg.argmax().view(1, 1)], 1)
+    hf_tokens = ids[0, n_prompt:].tolist()
+    caches = ours.new_caches(torch.float32)  # fp32 cache so the comparison is exact (test_tiny.py:58-60)
+    toks, errs = [], []
+    for s in range(0, n_prompt, C):
+        chunk = torch.zeros(1, C, dtype=torch.int32)
+        m = min(C, n_prompt - s)
+        chunk[0, :m] = prompt[0, s:s + m]
+        nxt, lg = ours.step(chunk, torch.tensor([s], dtype=torch.int32), torch.tensor([m - 1], dtype=torch.int32),
+                            caches, L)
+    toks.append(int(nxt))
+    errs.append((lg[0] - hf_logits[0]).abs().max().item())
+    for i in range(1, n_new):
+        nxt, lg = ours.step(nxt.view(1, 1), torch.tensor([n_prompt + i - 1], dtype=torch.int32),
+                            torch.tensor([0], dtype=torch.int32), caches, L)
+        toks.append(int(nxt))
+        errs.append((lg[0] - hf_logits[i]).abs().max().item())
+    return hf_tokens, toks, max(errs)
+
+
+def test_oracle_step_matches_transformers_reference_tiny():
+    hf_tokens, toks, err = _hf_vs_oracle(REF_TINY, 32, 64, 21, 10, 8, 32, 256)
+    assert toks == hf_tokens
+    assert err < 1e-3
+
+
+def test_oracle_step_matches_transformers_baseline_tiny_padded():
+    hf_tokens, toks, err = _hf_vs_oracle(BASELINE_TINY, 32, 128, 16, 12, 16, 64, 1024)
+    assert toks == hf_tokens
+    assert err < 1e-3
+
+
+def test_oracle_rope_tables_match_closed_form_default():
+    cos, sin = R.rope_tables(BASELINE_TINY, 32)
+    hd = 64
+    inv = 1.0 / (10000.0 ** (np.arange(0, hd, 2) / hd))
+    ang = np.arange(32)[:, None] * inv[None, :]
+    ang = np.concatenate([ang, ang], 1)
+    assert np.allclose(cos.numpy(), np.cos(ang), atol=2e-6)
+    assert np.allclose(sin.numpy(), np.sin(ang), atol=2e-6)
