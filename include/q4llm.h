@@ -83,13 +83,15 @@ int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x
  * F.linear(x, dequantize_q4(W))): y[M, N] = residual + x[M, K] @ dequant(W)^T, x and y fp32.
  * Runs on the fp16 matrix cores with x split into two fp16 terms and the int4 values exact in
  * fp16, the group scale applied in fp32 per K-group, so the result carries fp32-level accuracy.
- * Requires K % 32 == 0, group % 32 == 0, K % group == 0. residual: NULL or [M, N] fp32 (may alias y). */
+ * Requires K % 64 == 0, group % 32 == 0, K % group == 0, |x| < 65504. residual: NULL or [M, N] fp32
+ * (may alias y). */
 int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
               const float* residual, int64_t N, int64_t K, int group, void* stream);
 
 /* fp16 GEMM C[M,N] = A[M,K] @ B[N,K]^T ("NT", gemm/shapes.py:4-6, S2 prefill_nt), fp32
  * accumulation, fp16 output, row-major with leading dimensions lda/ldb/ldc (in elements).
- * Requires K % 8 == 0, lda/ldb % 8 == 0, 16-byte aligned A and B. */
+ * M == 1 runs a memory-bound fp16 GEMV. Requires K % 8 == 0, lda/ldb % 8 == 0, 16-byte aligned
+ * A and B. */
 int gemm_f16_nt(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, void* stream);
 
@@ -102,13 +104,14 @@ int attn_workspace_bytes(int C, int n_q, int n_kv, int hd, int L, size_t* bytes)
 
 /* GQA attention of C query rows at positions start[0] + c over k_cache/v_cache[:L]
  * (llama_q4.py:224-232): s = q . k * scale, keys with key_pos > pos masked (the reference's -1e30
- * fill), softmax in fp32, o = p . v. q [C, n_q, hd] fp32 (RoPE applied), caches
+ * fill), softmax in fp32, o = p . v. q: C rows of n_q * hd fp32 (RoPE applied) q_row_stride
+ * floats apart (n_q * hd when packed; the row pitch of a fused qkv buffer otherwise), caches
  * [>= L, n_kv, hd] fp16, out [C, n_q * hd] fp32. `start` is a device int32 (read by the kernels, so
  * the launch can be replayed from a graph). Split-K over the bucket length with a log-sum-exp
- * combine. Requires n_q % n_kv == 0, hd in {64, 128}, start + C <= L (checked on the device:
- * rows past L produce zeros). */
-int attn_bucket(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
-                int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
+ * combine. Requires n_q % n_kv == 0, hd in {64, 128}; keys at or beyond L are never read, so a
+ * position >= L attends to the whole bucket. */
+int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
+                float* out, int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
@@ -116,7 +119,7 @@ int attn_bucket(const float* q, const uint16_t* k_cache, const uint16_t* v_cache
  * ------------------------------------------------------------------------------------------- */
 
 /* rms_norm (llama_q4.py:141-142): out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w, rows of D fp32.
- * `row` NULL: all M rows; else the single row row[0] (device int32) of x -> out[0]. */
+ * `row` NULL: all M rows; else the single row row[0] (device int32, clamped to [0, M)) of x -> out[0]. */
 int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M, int64_t D, float eps,
                 const int32_t* row, void* stream);
 
@@ -186,12 +189,16 @@ int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t
 int q4_probe_read(const void* buf, int64_t bytes, float* sink, int loads_per_thread, void* stream);
 /* Empty kernel launch (launch-floor probe). */
 int q4_probe_empty(int grid, int block, void* stream);
-/* Number of entries in the explicit GEMV tile list, and q4_gemv with a forced entry (cfg < 0:
- * automatic) and grid (0: automatic). */
+/* Number of entries in the explicit GEMV / GEMM tile lists, and the same entry points with a
+ * forced entry (cfg < 0: automatic) and, for the GEMV, a grid (0: automatic; grid-stride entries
+ * only). gemm_f16_nt_cfg's `split` is reserved and must be 0. */
 int q4_gemv_num_configs(void);
 int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
                 int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg, int grid,
                 void* stream);
+int gemm_f16_num_configs(void);
+int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
+                    int64_t lda, int64_t ldb, int64_t ldc, int cfg, int split, void* stream);
 
 #ifdef __cplusplus
 }

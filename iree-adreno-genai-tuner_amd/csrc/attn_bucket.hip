@@ -1,0 +1,306 @@
+// KV-bucketed GQA attention for gfx950 (decode and chunked prefill share this kernel).
+//
+// Replaces the attention block of LlamaQ4.step (scripts/llm/llama_q4.py:204-232): for query row c
+// at position pos = start + c and query head h (KV head h / g), scores s = (q . k) * scale over
+// keys 0..L-1 of the position-first fp16 cache, keys with key_pos > pos masked (the reference fills
+// them with -1e30; exp of that minus any finite max is exactly 0 in fp32, so skipping them gives
+// the same softmax), softmax in fp32, o = p . v.
+//
+// Split-K over the bucket: workgroup (split, kv head, query block) handles S consecutive keys for
+// CB query rows x g query heads. It stages its queries and its V tile in LDS, computes the scores
+// with LPK = hd/8 lanes per key (one 16-byte K load per lane, DPP reduction across the LPK lanes),
+// takes the split-local max m and sum l of exp(s - m), and writes (m, l, o = sum exp(s - m) v) to
+// the workspace. The combine kernel merges the splits of each (row, head) with the log-sum-exp
+// rule. Splits whose first key lies past every query position of the block are skipped (decode
+// reads only the valid prefix of the bucket). `start` is read on the device.
+#include "q4_common.h"
+
+#include <cmath>
+
+namespace q4 {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;
+constexpr int kMaxQ = 64;  // queries (rows x group heads) per workgroup
+
+struct AttnPlan {
+  int S;         // keys per split
+  int CB;        // query rows per workgroup
+  int n_splits;  // ceil(L / S)
+  int n_cblk;    // ceil(C / CB)
+};
+
+AttnPlan plan_for(int C, int n_q, int n_kv, int L) {
+  const int g = n_q / n_kv;
+  AttnPlan p;
+  if (C == 1) {
+    p.CB = 1;
+    p.S = L <= 1024 ? 32 : (L <= 2048 ? 64 : 128);
+  } else {
+    p.CB = kMaxQ / g < C ? kMaxQ / g : C;
+    p.S = 64;
+  }
+  p.n_splits = (L + p.S - 1) / p.S;
+  p.n_cblk = (C + p.CB - 1) / p.CB;
+  return p;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float* f) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = half_bits_to_float(static_cast<uint16_t>(w[i] & 0xFFFFu));
+    f[2 * i + 1] = half_bits_to_float(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
+
+// LDS layout (floats): Q [nq][HD] | P [nq][S] | V tile [S][HD] as fp16 (uint4 rows)
+template <int HD, int S>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ ws_ml, float* __restrict__ ws_o, int C, int n_q, int n_kv, int L, int CB,
+    const int32_t* __restrict__ start_p, float scale, int q_stride) {
+  constexpr int LPK = HD / 8;          // lanes per key (8 halfs = 16 bytes each)
+  constexpr int KPI = 64 / LPK;        // keys per wave instruction
+  constexpr int KPW = S / 4;           // keys per wave
+  constexpr int NKI = KPW / KPI;       // key instructions per wave
+  static_assert(NKI >= 1, "split too small for the wave layout");
+  extern __shared__ float lds[];
+  const int g = n_q / n_kv;
+  const int split = blockIdx.x, hk = blockIdx.y, cb = blockIdx.z;
+  const int n_splits = gridDim.x;
+  const int k0 = split * S;
+  const int c0 = cb * CB;
+  const int rows = min(CB, C - c0);
+  const int nq = rows * g;
+  const int start = start_p[0];
+  float* Qs = lds;                                  // [nq][HD]
+  float* Ps = Qs + kMaxQ * HD;                      // [nq][S]
+  uint4* Vs = reinterpret_cast<uint4*>(Ps + kMaxQ * S);  // [S][HD/8]
+
+  // Split entirely past the last position of the block: empty partials.
+  const int last_pos = start + c0 + rows - 1;
+  const bool empty = k0 > last_pos;
+  if (empty) {
+    for (int i = threadIdx.x; i < nq; i += kThreads) {
+      const int c = c0 + i / g, h = hk * g + i % g;
+      const size_t idx = (static_cast<size_t>(c) * n_q + h) * n_splits + split;
+      ws_ml[2 * idx] = -INFINITY;
+      ws_ml[2 * idx + 1] = 0.0f;
+    }
+    return;  // the combine kernel never reads o of an empty split
+  }
+
+  const uint32_t cache_bytes = static_cast<uint32_t>(L) * n_kv * HD * 2u;
+  const __amdgpu_buffer_rsrc_t kres = make_rsrc(kc, cache_bytes);
+  const __amdgpu_buffer_rsrc_t vres = make_rsrc(vc, cache_bytes);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+  // 1. Issue this wave's K loads (rows past L are out of range: zeros) and the V tile loads.
+  uint4 kreg[NKI];
+#pragma unroll
+  for (int i = 0; i < NKI; ++i) {
+    const int key = k0 + wave * KPW + i * KPI + lane / LPK;
+    kreg[i] = buf_load16(kres, (static_cast<uint32_t>(key) * n_kv + hk) * (HD * 2u) + (lane % LPK) * 16u);
+  }
+  constexpr int VCH = S * HD / 8;  // 16-byte chunks in the V tile
+  uint4 vreg[(VCH + kThreads - 1) / kThreads];
+#pragma unroll
+  for (int i = 0; i < (VCH + kThreads - 1) / kThreads; ++i) {
+    const int ch = threadIdx.x + i * kThreads;
+    const int key = k0 + ch / LPK;
+    vreg[i] = buf_load16(vres, ch < VCH ? (static_cast<uint32_t>(key) * n_kv + hk) * (HD * 2u) + (ch % LPK) * 16u
+                                        : 0x80000000u);
+  }
+  // 2. Stage the queries (fp32) of this block: query i = (row c0 + i / g, head hk * g + i % g).
+  for (int e = threadIdx.x; e < nq * (HD / 4); e += kThreads) {
+    const int i = e / (HD / 4), d4 = e % (HD / 4);
+    const int c = c0 + i / g, h = hk * g + i % g;
+    reinterpret_cast<float4*>(Qs)[i * (HD / 4) + d4] =
+        reinterpret_cast<const float4*>(q + static_cast<size_t>(c) * q_stride + static_cast<size_t>(h) * HD)[d4];
+  }
+#pragma unroll
+  for (int i = 0; i < (VCH + kThreads - 1) / kThreads; ++i) {
+    const int ch = threadIdx.x + i * kThreads;
+    if (ch < VCH) Vs[ch] = vreg[i];
+  }
+  __syncthreads();
+
+  // 3. Scores: lane covers dims [8*(lane % LPK), +8) of key (lane / LPK); DPP sum over LPK lanes.
+#pragma unroll
+  for (int i = 0; i < NKI; ++i) {
+    const int kl = wave * KPW + i * KPI + lane / LPK;  // key index within the split
+    const int key = k0 + kl;
+    float kf[8];
+    unpack8(kreg[i], kf);
+    const int d0 = (lane % LPK) * 8;
+    for (int qi = 0; qi < nq; ++qi) {
+      const float4 a = reinterpret_cast<const float4*>(Qs + qi * HD + d0)[0];
+      const float4 b = reinterpret_cast<const float4*>(Qs + qi * HD + d0)[1];
+      float s = a.x * kf[0];
+      s = fmaf(a.y, kf[1], s);
+      s = fmaf(a.z, kf[2], s);
+      s = fmaf(a.w, kf[3], s);
+      s = fmaf(b.x, kf[4], s);
+      s = fmaf(b.y, kf[5], s);
+      s = fmaf(b.z, kf[6], s);
+      s = fmaf(b.w, kf[7], s);
+      s = segment_sum_to_last<LPK>(s);
+      if (lane % LPK == LPK - 1) {
+        const int pos = start + c0 + qi / g;
+        Ps[qi * S + kl] = (key <= pos && key < L) ? s * scale : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. Split-local softmax statistics: one wave per query, S / 64 keys per lane.
+  for (int qi = wave; qi < nq; qi += kThreads / 64) {
+    float m = -INFINITY;
+    for (int k = lane; k < S; k += 64) m = fmaxf(m, Ps[qi * S + k]);
+    m = group_max<64>(m);
+    float l = 0.0f;
+    for (int k = lane; k < S; k += 64) {
+      const float sv = Ps[qi * S + k];
+      const float p = sv == -INFINITY ? 0.0f : expf(sv - m);
+      Ps[qi * S + k] = p;
+      l += p;
+    }
+    l = group_sum<64>(l);
+    if (lane == 0) {
+      const int c = c0 + qi / g, h = hk * g + qi % g;
+      const size_t idx = (static_cast<size_t>(c) * n_q + h) * n_splits + split;
+      ws_ml[2 * idx] = m;
+      ws_ml[2 * idx + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // 5. o = sum_k p[q][k] v[k]: thread owns (query, 8-dim slice) pairs.
+  for (int pr = threadIdx.x; pr < nq * LPK; pr += kThreads) {
+    const int qi = pr / LPK, d8 = pr % LPK;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < S; ++k) {
+      const float p = Ps[qi * S + k];
+      float vf[8];
+      unpack8(Vs[k * LPK + d8], vf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(p, vf[j], acc[j]);
+    }
+    const int c = c0 + qi / g, h = hk * g + qi % g;
+    float* dst = ws_o + ((static_cast<size_t>(c) * n_q + h) * n_splits + split) * HD + d8 * 8;
+    reinterpret_cast<float4*>(dst)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    reinterpret_cast<float4*>(dst)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
+// Merge the splits of each (row, head): o = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
+// One workgroup of HD threads per (row, head); splits past the row's position are skipped.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
+                                                         float* __restrict__ out, int n_q, int n_splits, int S,
+                                                         const int32_t* __restrict__ start_p) {
+  const int c = blockIdx.x / n_q, h = blockIdx.x % n_q;
+  const int d = threadIdx.x;
+  const int pos = start_p[0] + c;
+  const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos
+  const size_t base = (static_cast<size_t>(c) * n_q + h) * n_splits;
+  float M = -INFINITY;
+  for (int i = 0; i < ns; ++i) M = fmaxf(M, ws_ml[2 * (base + i)]);
+  float num = 0.0f, den = 0.0f;
+  for (int i = 0; i < ns; ++i) {
+    const float m = ws_ml[2 * (base + i)];
+    if (m == -INFINITY) continue;
+    const float w = expf(m - M);
+    den = fmaf(w, ws_ml[2 * (base + i) + 1], den);
+    num = fmaf(w, ws_o[(base + i) * HD + d], num);
+  }
+  out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / den;
+}
+
+size_t lds_bytes(int HD, int S) {
+  return (static_cast<size_t>(kMaxQ) * HD + static_cast<size_t>(kMaxQ) * S) * 4 + static_cast<size_t>(S) * HD * 2;
+}
+
+template <int HD, int S>
+int launch_split(const AttnPlan& p, const float* q, int q_stride, const uint16_t* kc, const uint16_t* vc, float* ws_ml,
+                 float* ws_o, int C, int n_q, int n_kv, int L, const int32_t* start, float scale, hipStream_t st) {
+  const size_t lds = lds_bytes(HD, S);
+  if (lds > 64 * 1024) {
+    Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(attn_split_kernel<HD, S>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+  }
+  hipLaunchKernelGGL((attn_split_kernel<HD, S>), dim3(p.n_splits, n_kv, p.n_cblk), dim3(kThreads), lds, st, q, kc, vc,
+                     ws_ml, ws_o, C, n_q, n_kv, L, p.CB, start, scale, q_stride);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace q4
+
+using namespace q4;
+
+namespace {
+// (m, l) pairs of n partials, rounded up to 16 bytes so the o partials that follow stay aligned
+size_t ml_floats(size_t n) { return (2 * n + 3) / 4 * 4; }
+
+int attn_args(int C, int n_q, int n_kv, int hd, int L) {
+  if (C <= 0 || n_q <= 0 || n_kv <= 0 || L <= 0) return Q4_ERR_SHAPE;
+  if (n_q % n_kv) return Q4_ERR_SHAPE;
+  if (n_q / n_kv > kMaxQ) return Q4_ERR_UNSUPPORTED;
+  if (hd != 64 && hd != 128) return Q4_ERR_UNSUPPORTED;
+  if (static_cast<int64_t>(L) * n_kv * hd * 2 >= (int64_t{1} << 31)) return Q4_ERR_SHAPE;
+  return Q4_OK;
+}
+}  // namespace
+
+extern "C" int attn_workspace_bytes(int C, int n_q, int n_kv, int hd, int L, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (int st = attn_args(C, n_q, n_kv, hd, L)) return st;
+  const AttnPlan p = plan_for(C, n_q, n_kv, L);
+  const size_t n = static_cast<size_t>(C) * n_q * p.n_splits;
+  *bytes = ml_floats(n) * sizeof(float) + n * hd * sizeof(float);
+  return Q4_OK;
+}
+
+extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
+                           float* out, int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !start || !workspace) return Q4_ERR_NULL;
+  if (int st = attn_args(C, n_q, n_kv, hd, L)) return st;
+  if (q_row_stride < n_q * hd || q_row_stride % 4) return Q4_ERR_SHAPE;
+  size_t need = 0;
+  attn_workspace_bytes(C, n_q, n_kv, hd, L, &need);
+  if (workspace_bytes < need) return Q4_ERR_WORKSPACE;
+  if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(workspace, 16)) return Q4_ERR_ALIGN;
+  const AttnPlan p = plan_for(C, n_q, n_kv, L);
+  float* ws_ml = static_cast<float*>(workspace);
+  float* ws_o = ws_ml + ml_floats(static_cast<size_t>(C) * n_q * p.n_splits);
+  const hipStream_t st = as_stream(stream);
+  int rc;
+  if (hd == 128) {
+    if (p.S == 32) rc = launch_split<128, 32>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+    else if (p.S == 64) rc = launch_split<128, 64>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+    else rc = launch_split<128, 128>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+  } else {
+    if (p.S == 32) rc = launch_split<64, 32>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+    else if (p.S == 64) rc = launch_split<64, 64>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+    else rc = launch_split<64, 128>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
+  }
+  if (rc) return rc;
+  if (hd == 128)
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(C * n_q), dim3(128), 0, st, ws_ml, ws_o, out, n_q, p.n_splits, p.S, start);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(C * n_q), dim3(64), 0, st, ws_ml, ws_o, out, n_q, p.n_splits, p.S, start);
+  return launch_status();
+}

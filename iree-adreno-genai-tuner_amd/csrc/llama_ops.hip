@@ -1,0 +1,207 @@
+// Element-wise, normalisation and selection kernels of LlamaQ4.step
+// (scripts/llm/llama_q4.py:141-142, 194-239).
+//
+// Floating-point contraction is disabled in this file so that each multiply and add rounds like
+// the reference's separate tensor ops (x * cos + rotate_half(x) * sin, x * r * w, ...); with the
+// same operation order the element-wise results are bit-identical to the CPU ops, and only the
+// reductions (sum of squares, exp) differ in the last bits.
+#include "q4_common.h"
+
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace q4 {
+namespace {
+
+// rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
+// mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      float* __restrict__ out, int64_t M, int64_t D, float eps,
+                                                      const int32_t* __restrict__ row_sel) {
+  // a selected row outside [0, M) is clamped (the reference's index_select would raise)
+  const int64_t row = row_sel ? min(max(static_cast<int64_t>(row_sel[0]), int64_t{0}), M - 1) : blockIdx.x;
+  const float* xr = x + row * D;
+  float* orow = out + static_cast<int64_t>(blockIdx.x) * D;
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    const float v = xr[i];
+    const float sq = v * v;
+    s += sq;
+  }
+  s = group_sum<64>(s);
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float mean = total / static_cast<float>(D);
+  const float r = 1.0f / sqrtf(mean + eps);
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    const float t = xr[i] * r;
+    orow[i] = t * w[i];
+  }
+}
+
+// RoPE on q and k of qkv rows (in place) and the fp16 KV row writes, one thread per (row, head,
+// d < hd/2) pair; rotate_half(x) = cat(-x[hd/2:], x[:hd/2]) (llama_q4.py:194-197).
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, const float* __restrict__ cos_t,
+                                                      const float* __restrict__ sin_t, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc, int C, int n_q, int n_kv, int hd,
+                                                      int max_ctx, const int32_t* __restrict__ start_p) {
+  const int half = hd / 2;
+  const int heads = n_q + 2 * n_kv;
+  const int64_t total = static_cast<int64_t>(C) * heads * half;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int d = static_cast<int>(t % half);
+  const int head = static_cast<int>((t / half) % heads);
+  const int c = static_cast<int>(t / (static_cast<int64_t>(half) * heads));
+  const int pos = start_p[0] + c;
+  if (pos < 0 || pos >= max_ctx) return;
+  float* row = qkv + (static_cast<int64_t>(c) * heads + head) * hd;
+  const float x1 = row[d], x2 = row[d + half];
+  if (head < n_q + n_kv) {  // q or k: rotate
+    const float* cp = cos_t + static_cast<int64_t>(pos) * hd;
+    const float* sp = sin_t + static_cast<int64_t>(pos) * hd;
+    const float a = x1 * cp[d];
+    const float b = (-x2) * sp[d];
+    const float lo = a + b;
+    const float e = x2 * cp[d + half];
+    const float f = x1 * sp[d + half];
+    const float hi = e + f;
+    if (head < n_q) {
+      row[d] = lo;
+      row[d + half] = hi;
+    } else {
+      row[d] = lo;
+      row[d + half] = hi;
+      uint16_t* dst = kc + (static_cast<int64_t>(pos) * n_kv + (head - n_q)) * hd;
+      dst[d] = float_to_half_bits(lo);
+      dst[d + half] = float_to_half_bits(hi);
+    }
+  } else {  // v: copy into the cache
+    uint16_t* dst = vc + (static_cast<int64_t>(pos) * n_kv + (head - n_q - n_kv)) * hd;
+    dst[d] = float_to_half_bits(x1);
+    dst[d + half] = float_to_half_bits(x2);
+  }
+}
+
+// silu(g) * u with silu(x) = x / (1 + exp(-x)) (F.silu), gu = [M, 2 * inter] (gate then up).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu, float* __restrict__ out,
+                                                       int64_t M, int64_t inter) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= M * inter) return;
+  const int64_t m = t / inter, i = t % inter;
+  const float g = gu[m * 2 * inter + i];
+  const float u = gu[m * 2 * inter + inter + i];
+  const float e = expf(-g);
+  const float den = 1.0f + e;
+  const float sg = g / den;
+  out[t] = sg * u;
+}
+
+// argmax with torch.argmax semantics: the first index of the maximum; a NaN counts as the maximum
+// (the first NaN wins).
+struct Best {
+  float v;
+  int32_t i;
+};
+
+__device__ __forceinline__ bool better(float a, int32_t ia, float b, int32_t ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+__device__ __forceinline__ Best block_best(Best b) {
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(b.v, m, 64);
+    const int32_t oi = __shfl_xor(b.i, m, 64);
+    if (better(ov, oi, b.v, b.i)) { b.v = ov; b.i = oi; }
+  }
+  __shared__ float sv[4];
+  __shared__ int32_t si[4];
+  if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = b.v; si[threadIdx.x >> 6] = b.i; }
+  __syncthreads();
+  Best r{sv[0], si[0]};
+  for (int w = 1; w < 4; ++w)
+    if (better(sv[w], si[w], r.v, r.i)) { r.v = sv[w]; r.i = si[w]; }
+  return r;
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int64_t V,
+                                                             Best* __restrict__ ws) {
+  Best b{-INFINITY, INT32_MAX};
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < V; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const float v = x[i];
+    if (better(v, static_cast<int32_t>(i), b.v, b.i)) { b.v = v; b.i = static_cast<int32_t>(i); }
+  }
+  const Best r = block_best(b);
+  if (threadIdx.x == 0) ws[blockIdx.x] = r;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const Best* __restrict__ ws, int n, int32_t* __restrict__ out) {
+  Best b{-INFINITY, INT32_MAX};
+  for (int i = threadIdx.x; i < n; i += 256)
+    if (better(ws[i].v, ws[i].i, b.v, b.i)) b = ws[i];
+  const Best r = block_best(b);
+  if (threadIdx.x == 0) out[0] = r.i;
+}
+
+int argmax_blocks(int64_t V) {
+  const int64_t b = (V + 256 * 16 - 1) / (256 * 16);
+  return static_cast<int>(b < 1 ? 1 : (b > 512 ? 512 : b));
+}
+
+}  // namespace
+}  // namespace q4
+
+using namespace q4;
+
+extern "C" int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M, int64_t D, float eps,
+                           const int32_t* row, void* stream) {
+  if (!x || !w || !out) return Q4_ERR_NULL;
+  if (M <= 0 || D <= 0) return Q4_ERR_SHAPE;
+  const unsigned grid = row ? 1u : static_cast<unsigned>(M);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row);
+  return launch_status();
+}
+
+extern "C" int rope_kv_write(float* qkv, const float* cos_t, const float* sin_t, uint16_t* k_cache, uint16_t* v_cache,
+                             int C, int n_q, int n_kv, int hd, int max_ctx, const int32_t* start, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !k_cache || !v_cache || !start) return Q4_ERR_NULL;
+  if (C <= 0 || n_q <= 0 || n_kv <= 0 || hd <= 0 || hd % 2 || max_ctx <= 0) return Q4_ERR_SHAPE;
+  const int64_t total = static_cast<int64_t>(C) * (n_q + 2 * n_kv) * (hd / 2);
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     qkv, cos_t, sin_t, k_cache, v_cache, C, n_q, n_kv, hd, max_ctx, start);
+  return launch_status();
+}
+
+extern "C" int silu_mul_f32(const float* gu, float* out, int64_t M, int64_t inter, void* stream) {
+  if (!gu || !out) return Q4_ERR_NULL;
+  if (M <= 0 || inter <= 0) return Q4_ERR_SHAPE;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((M * inter + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), gu, out, M, inter);
+  return launch_status();
+}
+
+extern "C" int argmax_workspace_bytes(int64_t V, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (V <= 0 || V > INT32_MAX) return Q4_ERR_SHAPE;
+  *bytes = static_cast<size_t>(argmax_blocks(V)) * sizeof(Best);
+  return Q4_OK;
+}
+
+extern "C" int argmax_f32(const float* logits, int64_t V, int32_t* out, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (!logits || !out || !workspace) return Q4_ERR_NULL;
+  size_t need = 0;
+  if (int st = argmax_workspace_bytes(V, &need)) return st;
+  if (workspace_bytes < need) return Q4_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return Q4_ERR_ALIGN;
+  const int nb = argmax_blocks(V);
+  const hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(nb), dim3(256), 0, st, logits, V, static_cast<Best*>(workspace));
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, static_cast<const Best*>(workspace), nb, out);
+  return launch_status();
+}

@@ -1,0 +1,142 @@
+// One LlamaQ4 step (scripts/llm/llama_q4.py:199-239) as a sequence of gfx950 kernels on one stream.
+//
+// This is the body of the reference's exported entry points prefill_c{C}_l{L} / decode_l{L} /
+// decode_logits_l{L} (scripts/llm/export_llama.py:35-49): tokens, start and last are device buffers
+// and every kernel reads them on the device, so one (C, L) step can be captured once into a HIP
+// graph and replayed for every call of that entry point. Nothing here allocates or synchronises;
+// activations live in the caller's workspace, the KV caches are the caller's and are written in place.
+//
+// Per layer (x fp32 activations, as the reference):
+//   x = rms_norm(h, ln_in); qkv = x W_qkv^T; RoPE(q, k) + fp16 K/V rows at start..start+C-1;
+//   o = attention over cache[:L]; h = h + o W_o^T; x = rms_norm(h, ln_post); gu = x W_gu^T;
+//   h = h + (silu(gate) * up) W_down^T
+// then x = rms_norm(h[last], ln_f), logits = x E^T (tied int4 embedding), next = argmax(logits).
+// Projections: C == 1 -> q4_gemv (fp32 in/out, residual fused); C > 1 -> q4_linear (fused int4
+// MFMA GEMM with split-fp16 activations and per-group fp32 scales, residual fused).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+
+#include "q4llm.h"
+
+namespace {
+
+struct Layout {
+  size_t h, x, qkv, o, gu, act, xf, logits, attn, amax, total;
+  size_t attn_bytes, amax_bytes;
+};
+
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
+  const size_t f = sizeof(float);
+  const int nq = m->n_heads * m->head_dim, nkv = m->n_kv * m->head_dim;
+  size_t attn = 0, amax = 0;
+  if (int st = attn_workspace_bytes(C, m->n_heads, m->n_kv, m->head_dim, L, &attn)) return st;
+  if (int st = argmax_workspace_bytes(m->vocab, &amax)) return st;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t o = off; off += up256(bytes); return o; };
+  lo->h = take(f * C * m->dim);
+  lo->x = take(f * C * m->dim);
+  lo->qkv = take(f * C * (nq + 2 * nkv));
+  lo->o = take(f * C * nq);
+  lo->gu = take(f * C * 2 * m->inter);
+  lo->act = take(f * C * m->inter);
+  lo->xf = take(f * m->dim);
+  lo->logits = take(f * m->vocab);
+  lo->attn = take(attn);
+  lo->amax = take(amax);
+  lo->attn_bytes = attn;
+  lo->amax_bytes = amax;
+  lo->total = off;
+  return Q4_OK;
+}
+
+int check_model(const q4llm_model* m) {
+  if (!m || !m->layers || !m->embed_q || !m->embed_s || !m->ln_f || !m->cos_t || !m->sin_t) return Q4_ERR_NULL;
+  if (m->dim <= 0 || m->n_layers <= 0 || m->n_heads <= 0 || m->n_kv <= 0 || m->head_dim <= 0 || m->inter <= 0 ||
+      m->vocab <= 0 || m->group <= 0 || m->max_ctx <= 0)
+    return Q4_ERR_SHAPE;
+  if (m->n_heads % m->n_kv) return Q4_ERR_SHAPE;
+  for (int i = 0; i < m->n_layers; ++i) {
+    const q4llm_layer& l = m->layers[i];
+    if (!l.wqkv_q || !l.wqkv_s || !l.wo_q || !l.wo_s || !l.wgu_q || !l.wgu_s || !l.wdown_q || !l.wdown_s ||
+        !l.ln_in || !l.ln_post)
+      return Q4_ERR_NULL;
+  }
+  return Q4_OK;
+}
+
+// y = residual + x W^T for C rows (C == 1: GEMV, else fused int4 GEMM).
+int proj(int C, const float* x, const int32_t* q, const uint16_t* s, float* y, const float* res, int N, int K, int group,
+         void* stream) {
+  if (C == 1) return q4_gemv(q, s, x, Q4_F32, y, Q4_F32, res, N, K, group, stream);
+  return q4_linear(x, C, q, s, y, res, N, K, group, stream);
+}
+
+}  // namespace
+
+extern "C" int q4llm_step_workspace_bytes(const q4llm_model* m, int C, int L, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (int st = check_model(m)) return st;
+  if (C <= 0 || L <= 0 || L > m->max_ctx || C > m->max_ctx) return Q4_ERR_RANGE;
+  Layout lo;
+  if (int st = layout_for(m, C, L, &lo)) return st;
+  *bytes = lo.total;
+  return Q4_OK;
+}
+
+extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start, const int32_t* last,
+                          void* const* caches, int L, int32_t* next, float* logits, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (int st = check_model(m)) return st;
+  if (!tokens || !start || !last || !caches || !next || !workspace) return Q4_ERR_NULL;
+  if (C <= 0 || L <= 0 || L > m->max_ctx || C > m->max_ctx) return Q4_ERR_RANGE;
+  for (int i = 0; i < 2 * m->n_layers; ++i)
+    if (!caches[i]) return Q4_ERR_NULL;
+  Layout lo;
+  if (int st = layout_for(m, C, L, &lo)) return st;
+  if (workspace_bytes < lo.total) return Q4_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  float* h = reinterpret_cast<float*>(ws + lo.h);
+  float* x = reinterpret_cast<float*>(ws + lo.x);
+  float* qkv = reinterpret_cast<float*>(ws + lo.qkv);
+  float* o = reinterpret_cast<float*>(ws + lo.o);
+  float* gu = reinterpret_cast<float*>(ws + lo.gu);
+  float* act = reinterpret_cast<float*>(ws + lo.act);
+  float* xf = reinterpret_cast<float*>(ws + lo.xf);
+  float* lg = logits ? logits : reinterpret_cast<float*>(ws + lo.logits);
+  void* attn_ws = ws + lo.attn;
+  void* amax_ws = ws + lo.amax;
+
+  const int D = m->dim, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv;
+  const int nq_w = nh * hd, qkv_w = (nh + 2 * nkv) * hd;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+#define Q4_TRY(expr)            \
+  do {                          \
+    const int st_ = (expr);     \
+    if (st_ != Q4_OK) return st_; \
+  } while (0)
+
+  Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
+  for (int i = 0; i < m->n_layers; ++i) {
+    const q4llm_layer& ly = m->layers[i];
+    uint16_t* kc = static_cast<uint16_t*>(caches[2 * i]);
+    uint16_t* vc = static_cast<uint16_t*>(caches[2 * i + 1]);
+    Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
+    Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, stream));
+    Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
+    Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
+    Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, stream));
+    Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
+    Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, stream));
+    Q4_TRY(silu_mul_f32(gu, act, C, m->inter, stream));
+    Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, stream));
+  }
+  Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
+  Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
+  Q4_TRY(argmax_f32(lg, m->vocab, next, amax_ws, lo.amax_bytes, stream));
+#undef Q4_TRY
+  return Q4_OK;
+}

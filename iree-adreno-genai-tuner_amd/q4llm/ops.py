@@ -111,16 +111,18 @@ def attn_workspace_bytes(C_rows, n_q, n_kv, hd, L) -> int:
 
 
 def attn_bucket(q, k_cache, v_cache, L, start, scale, workspace=None, out=None):
-    """Attention of q [C, n_q, hd] (fp32) at positions start+c over caches [:L] (fp16)."""
+    """Attention of q [C, n_q, hd] (fp32, rows may be strided) at positions start+c over caches [:L]."""
     _dev(q, k_cache, v_cache, start)
     c, n_q, hd = q.shape
+    if q.stride(2) != 1 or q.stride(1) != hd:
+        q = q.contiguous()
     n_kv = k_cache.shape[1]
     ws_bytes = attn_workspace_bytes(c, n_q, n_kv, hd, L)
     if workspace is None:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     if out is None:
         out = torch.empty(c, n_q * hd, dtype=torch.float32, device=q.device)
-    LIB.call("attn_bucket", ptr(q.contiguous()), ptr(k_cache), ptr(v_cache), ptr(out), c, n_q, n_kv, hd, L,
+    LIB.call("attn_bucket", ptr(q), q.stride(0), ptr(k_cache), ptr(v_cache), ptr(out), c, n_q, n_kv, hd, L,
              ptr(start), scale, ptr(workspace), workspace.numel(), stream_of(q.device))
     return out
 

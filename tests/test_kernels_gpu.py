@@ -1,0 +1,210 @@
+"""GPU parity of attention, the fp16 GEMM, the fused int4 prefill GEMM and the support ops against
+CPU references (fp64 textbook forms and the oracle). Tolerances are written per test; outputs are
+NaN-poisoned before each kernel runs."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import llama_q4_ref as R
+from q4llm import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def nan_like(shape, dtype, dev):
+    return torch.full(shape, float("nan"), dtype=dtype, device=dev)
+
+
+# ------------------------------------------------------------------------------------------------
+# attention over a KV bucket (llama_q4.py:224-232)
+# ------------------------------------------------------------------------------------------------
+
+
+def attn_ref(q, kc, vc, start, L, scale):
+    """fp64 brute force: q [C, nq, hd], caches [>=L, nkv, hd] (fp16 values), key <= pos masked."""
+    Cn, nq, hd = q.shape
+    nkv = kc.shape[1]
+    g = nq // nkv
+    K = kc[:L].double()
+    V = vc[:L].double()
+    out = torch.zeros(Cn, nq, hd, dtype=torch.float64)
+    for c in range(Cn):
+        pos = start + c
+        n = min(L, pos + 1)
+        for h in range(nq):
+            s = (K[:n, h // g] @ q[c, h].double()) * scale
+            p = torch.softmax(s, 0)
+            out[c, h] = p @ V[:n, h // g]
+    return out.reshape(Cn, nq * hd)
+
+
+@pytest.mark.parametrize("L", [256, 512, 1024, 2048, 4096])
+def test_attn_decode_config4(dev, L):
+    q, k, v, valid = synth.attn_problem(L, seed=L)
+    kc, vc = torch.from_numpy(k), torch.from_numpy(v)
+    qt = torch.from_numpy(q)
+    start = valid - 1
+    ref = attn_ref(qt, kc, vc, start, L, 1 / math.sqrt(128))
+    out = nan_like((1, 24 * 128), torch.float32, dev)
+    ops.attn_bucket(qt.to(dev), kc.to(dev), vc.to(dev), L, torch.tensor([start], dtype=torch.int32, device=dev),
+                    1 / math.sqrt(128), out=out)
+    err = (out.cpu().double() - ref).abs().max().item()
+    assert err < 2e-5, (L, valid, err)
+
+
+@pytest.mark.parametrize("start,L", [(0, 64), (5, 64), (63, 64), (100, 128), (4095, 4096)])
+def test_attn_decode_edges(dev, start, L):
+    """Single valid key, last slot of the bucket, and stale rows past pos (must be ignored)."""
+    g = torch.Generator().manual_seed(start + L)
+    q = torch.randn(1, 8, 128, generator=g)
+    kc = torch.randn(L, 2, 128, generator=g).half()
+    vc = torch.randn(L, 2, 128, generator=g).half()
+    ref = attn_ref(q, kc, vc, start, L, 0.088)
+    out = ops.attn_bucket(q.to(dev), kc.to(dev), vc.to(dev), L, torch.tensor([start], dtype=torch.int32, device=dev), 0.088)
+    assert (out.cpu().double() - ref).abs().max().item() < 2e-5
+    if start == 0:  # one key: the output is that key's value row exactly (up to fp32 rounding)
+        assert torch.allclose(out.cpu().reshape(8, 128), vc[0].float().repeat_interleave(4, 0), atol=1e-6)
+
+
+@pytest.mark.parametrize("Cn,start,L,nq,nkv,hd", [(256, 0, 256, 24, 8, 128), (256, 256, 512, 24, 8, 128),
+                                                  (16, 0, 64, 4, 2, 64), (8, 13, 32, 8, 2, 32 * 2), (5, 3, 64, 4, 2, 64)])
+def test_attn_prefill_chunk(dev, Cn, start, L, nq, nkv, hd):
+    g = torch.Generator().manual_seed(Cn + start)
+    qkv_w = (nq + 2 * nkv) * hd
+    qkv = torch.randn(Cn, qkv_w, generator=g)
+    kc = torch.randn(L, nkv, hd, generator=g).half()
+    vc = torch.randn(L, nkv, hd, generator=g).half()
+    q = qkv[:, : nq * hd].reshape(Cn, nq, hd)
+    ref = attn_ref(q, kc, vc, start, L, 1 / math.sqrt(hd))
+    qd = qkv.to(dev)[:, : nq * hd].reshape(Cn, nq, hd)  # strided rows of the fused qkv buffer
+    out = ops.attn_bucket(qd, kc.to(dev), vc.to(dev), L, torch.tensor([start], dtype=torch.int32, device=dev),
+                          1 / math.sqrt(hd))
+    assert (out.cpu().double() - ref).abs().max().item() < 2e-5
+
+
+# ------------------------------------------------------------------------------------------------
+# fp16 GEMM (gemm/shapes.py contract)
+# ------------------------------------------------------------------------------------------------
+
+GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 5120, 3072), (2048, 3072, 8192),
+               (4096, 4096, 4096), (1, 3072, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_config3(dev, M, N, K):
+    a, b = synth.gemm_problem(M, N, K, seed=1)
+    A, B = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    c = nan_like((M, N), torch.float16, dev)
+    ops.gemm_f16_nt(A, B, out=c)
+    ref = A.float() @ B.float().T  # fp32 reference of the fp16 inputs (gemm/shapes.py:62)
+    rms = ref.pow(2).mean().sqrt().item()
+    err = (c.float() - ref).abs().max().item()
+    assert err <= 1e-2 * rms, (err, rms)
+
+
+@pytest.mark.parametrize("sid,M,N,K", [("S2", 128, 3072, 3072), ("S4", 16, 4096, 4096), ("S7", 1, 4096, 4096)])
+def test_gemm_reference_nt_shapes_tol(dev, sid, M, N, K):
+    """The reference's NT shapes with its own data recipe and TOL (gemm/shapes.py:41-66):
+    U(-1,1) from default_rng(seed + id), max|C - Cref| / max|Cref| <= 5e-3."""
+    rng = np.random.default_rng(0 + int(sid[1:]))
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float16)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float16)
+    cref = a.astype(np.float32) @ b.astype(np.float32)
+    A = torch.from_numpy(a).to(dev)
+    Bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(dev)  # stored transposed: [N, K]
+    c = ops.gemm_f16_nt(A, Bt).float().cpu().numpy()
+    assert np.abs(c - cref).max() / np.abs(cref).max() <= 5e-3
+
+
+def test_gemm_all_tiles_and_ragged_edges(dev):
+    from q4llm._lib import LIB
+    n_cfg = LIB.raw("gemm_f16_num_configs")()
+    for (M, N, K) in [(200, 300, 136), (64, 64, 64), (33, 257, 520)]:
+        a, b = synth.gemm_problem(M, N, K, seed=2)
+        A, B = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+        ref = A.float() @ B.float().T
+        for cfg in range(n_cfg):
+            c = nan_like((M, N), torch.float16, dev)
+            ops.gemm_f16_nt_cfg(A, B, c, cfg=cfg)
+            assert (c.float() - ref).abs().max().item() <= 1e-2 * ref.pow(2).mean().sqrt().item(), (M, N, K, cfg)
+
+
+# ------------------------------------------------------------------------------------------------
+# fused int4 prefill GEMM (QLinear.forward at M > 1)
+# ------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("M,N,K,group", [(256, 5120, 3072, 128), (256, 3072, 8192, 128), (16, 1408, 256, 32),
+                                         (16, 256, 704, 32), (7, 100, 128, 64), (300, 3072, 3072, 128)])
+def test_q4_linear_fp32_accuracy(dev, M, N, K, group):
+    g = torch.Generator().manual_seed(M + N)
+    w = torch.randn(N, K, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g)
+    res = torch.randn(M, N, generator=g)
+    qw, sc = R.quantize_q4(w, group)
+    ref = x.double() @ R.dequantize_q4(qw, sc, group).double().T
+    rms = ref.pow(2).mean().sqrt().item()
+    y = ops.q4_linear(x.to(dev), qw.to(dev), sc.to(dev), group)
+    assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+    h = res.to(dev).clone()
+    ops.q4_linear(x.to(dev), qw.to(dev), sc.to(dev), group, residual=h, out=h)
+    assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
+
+
+# ------------------------------------------------------------------------------------------------
+# support ops
+# ------------------------------------------------------------------------------------------------
+
+
+def test_rmsnorm_and_row_select(dev):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 3072, generator=g) * 3
+    w = torch.randn(3072, generator=g)
+    ref = R.rms_norm(x, w, 1e-5)
+    out = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu()
+    assert torch.allclose(out, ref, rtol=2e-6, atol=1e-6)
+    one = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, row=torch.tensor([3], dtype=torch.int32, device=dev)).cpu()
+    assert torch.allclose(one[0], ref[3], rtol=2e-6, atol=1e-6)
+
+
+def test_rope_kv_write_bit_exact(dev):
+    nq, nkv, hd, Cn, start = 4, 2, 64, 6, 9
+    g = torch.Generator().manual_seed(8)
+    qkv = torch.randn(Cn, (nq + 2 * nkv) * hd, generator=g)
+    cos, sin = R.rope_tables(dict(hidden_size=256, num_attention_heads=nq, num_key_value_heads=nkv, head_dim=hd,
+                                  rope_theta=10000.0, max_position_embeddings=64), 64)
+    pos = torch.arange(start, start + Cn)
+    q = qkv[:, : nq * hd].reshape(Cn, nq, hd)
+    k = qkv[:, nq * hd: (nq + nkv) * hd].reshape(Cn, nkv, hd)
+    v = qkv[:, (nq + nkv) * hd:].reshape(Cn, nkv, hd)
+    cs, sn = cos[pos][:, None], sin[pos][:, None]
+    q_ref = q * cs + R.rotate_half(q) * sn
+    k_ref = k * cs + R.rotate_half(k) * sn
+    kc = torch.zeros(64, nkv, hd, dtype=torch.float16, device=dev)
+    vc = torch.zeros(64, nkv, hd, dtype=torch.float16, device=dev)
+    qd = qkv.to(dev)
+    ops.rope_kv_write(qd, cos.to(dev), sin.to(dev), kc, vc, nq, nkv, hd, torch.tensor([start], dtype=torch.int32, device=dev))
+    assert torch.equal(qd.cpu()[:, : nq * hd].reshape(Cn, nq, hd), q_ref)
+    assert torch.equal(kc.cpu()[start:start + Cn], k_ref.half())
+    assert torch.equal(vc.cpu()[start:start + Cn], v.half())
+    assert kc.cpu()[:start].abs().sum() == 0 and kc.cpu()[start + Cn:].abs().sum() == 0
+
+
+def test_silu_mul(dev):
+    g = torch.Generator().manual_seed(9)
+    gu = torch.randn(3, 2 * 704, generator=g) * 4
+    ref = torch.nn.functional.silu(gu[:, :704]) * gu[:, 704:]
+    out = ops.silu_mul(gu.to(dev), 704).cpu()
+    assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("V", [1, 1000, 128256])
+def test_argmax_first_max(dev, V):
+    g = torch.Generator().manual_seed(V)
+    x = torch.randn(V, generator=g)
+    if V > 10:
+        x[V // 3] = x[V - 2] = x.max() + 1.0  # tie: the first index wins
+    assert int(ops.argmax(x.to(dev)).item()) == int(torch.argmax(x).item())

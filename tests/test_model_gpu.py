@@ -1,0 +1,108 @@
+"""Whole-model parity on the GPU: LlamaQ4.step and the runner against the CPU oracle on the tiny
+configs (exact greedy tokens; logits within the reference's per-op tolerance
+1e-3 * max(1, max|ref|), scripts/debug/op_test.py:74-77), plus graph replay consistency.
+Both sides keep fp16 KV caches, so the logit difference comes from rare one-ulp rounding flips of
+cache entries whose fp32 values differ in the last bits."""
+
+import json
+import pathlib
+
+import pytest
+import torch
+
+from oracle import llama_q4_ref as R
+from q4llm import llm_runner, synth
+from q4llm.llama_q4 import LlamaQ4
+
+pytestmark = pytest.mark.gpu
+GOLD = pathlib.Path(__file__).parent / "golden"
+
+
+def build_pair(cfg, group, max_ctx, seed=0, std=0.2):
+    sd = synth.SyntheticWeights(cfg, seed, std=std)
+    dense = {k: sd[k] for k in sd.keys()}
+    ours = LlamaQ4(None, group=group, max_ctx=max_ctx, sd=dense, cfg=cfg)
+    ref = R.LlamaQ4Ref(cfg, dense, group=group, max_ctx=max_ctx, rope=(ours.cos.cpu(), ours.sin.cpu()))
+    return ours, ref
+
+
+def tol(ref):
+    return 1e-3 * max(1.0, ref.abs().max().item())
+
+
+def test_quantized_weights_bit_exact(dev):
+    ours, ref = build_pair(synth.TINY, 32, 128)
+    assert torch.equal(ours.embed.qweight.cpu(), ref.embed.qweight)
+    for lo, lr in zip(ours.layers, ref.layers):
+        for name in ("wqkv", "wo", "wgu", "wdown"):
+            assert torch.equal(getattr(lo, name).qweight.cpu(), lr[name].qweight), name
+            assert torch.equal(getattr(lo, name).scales.cpu().view(torch.int16), lr[name].scales.view(torch.int16))
+
+
+def test_step_prefill_and_decode_vs_oracle(dev):
+    ours, ref = build_pair(synth.TINY, 32, 128)
+    prompt = synth.prompt_ids(16, 1024, seed=0)
+    ours_c, ref_c = ours.new_caches(), ref.new_caches()
+    toks = torch.tensor([prompt], dtype=torch.int32)
+    n1, l1 = ours.step(toks, torch.tensor([0], dtype=torch.int32), torch.tensor([15], dtype=torch.int32), ours_c, 64)
+    r1, rl1 = ref.step(toks, torch.tensor([0], dtype=torch.int32), torch.tensor([15], dtype=torch.int32), ref_c, 64)
+    assert int(n1.item()) == int(r1.item())
+    assert (l1.cpu() - rl1).abs().max().item() <= tol(rl1)
+    # Caches written in place: both sides round fp32 K/V to fp16; fp32 differences in the last bits
+    # (growing slightly through the layers) flip a few roundings. Layer 0 differs by at most one
+    # fp16 ulp where the value is not tiny; every layer stays within 2e-3 of the cache's max.
+    for i in range(8):
+        a, b = ours_c[i].cpu(), ref_c[i]
+        if i < 2:
+            big = b.float().abs() >= 2.0 ** -6
+            ulps = (a.view(torch.int16).int() - b.view(torch.int16).int()).abs()
+            assert ulps[big].max().item() <= 1
+        assert (a.float() - b.float()).abs().max().item() <= 2e-3 * b.float().abs().max().item()
+    nxt, rn = n1, r1
+    for pos in range(16, 24):
+        nxt, lg = ours.step(nxt.reshape(1, 1).cpu(), torch.tensor([pos], dtype=torch.int32),
+                            torch.tensor([0], dtype=torch.int32), ours_c, 64)
+        rn, rlg = ref.step(rn.reshape(1, 1), torch.tensor([pos], dtype=torch.int32), torch.tensor([0], dtype=torch.int32),
+                           ref_c, 64)
+        assert int(nxt.item()) == int(rn.item())
+        assert (lg.cpu() - rlg).abs().max().item() <= tol(rlg)
+
+
+@pytest.mark.parametrize("variant", ["baseline_std0.02", "std0.2"])
+def test_tiny_generation_matches_golden(dev, variant):
+    """16-token prompt, 32 greedy tokens, buckets {64, 128}, chunk 16 (weights
+    N(0, 0.02) as stated, and N(0, 0.2) whose greedy tokens vary)."""
+    gold = json.loads((GOLD / "tiny_tokens.json").read_text())[variant]
+    sd = synth.SyntheticWeights(synth.TINY, gold["seed"], std=gold["std"])
+    model = LlamaQ4(None, group=gold["group"], max_ctx=gold["max_ctx"], sd=sd, cfg=synth.TINY)
+    res = llm_runner.run(model, gold["prompt"], gold["max_new_tokens"], gold["chunk"], gold["buckets"])
+    assert res["tokens"] == gold["tokens"]
+    assert res["new_tokens"] == gold["max_new_tokens"] and res["decode_steps"] == gold["max_new_tokens"] - 1
+
+
+def test_runner_ragged_prompt_and_stop_ids(dev):
+    model, ref = build_pair(synth.TINY, 32, 128)
+    prompt = synth.prompt_ids(21, 1024, seed=3)
+    want = R.generate(ref, prompt, 10, 8, [16, 32, 64])
+    res = llm_runner.run(model, prompt, 10, 8, [16, 32, 64])
+    assert res["tokens"] == want
+    assert [L for L, _ in res["chunks"]] == [16, 16, 32]
+    stop = want[3]
+    res2 = llm_runner.run(model, prompt, 10, 8, [16, 32, 64], stop_ids={stop})
+    assert res2["tokens"] == want[: want.index(stop) + 1]
+
+
+def test_graph_replay_matches_eager_step(dev):
+    """The captured entry point, replayed several times with eager work in between, equals step()."""
+    model, _ = build_pair(synth.TINY, 32, 128)
+    caches_g, caches_e = model.new_caches(), model.new_caches()
+    fn = model.entry_point(1, 64, caches_g, logits=True)
+    for pos, tok in [(0, 5), (1, 17), (2, 900), (3, 3)]:
+        lg = fn([tok], pos, 0).clone()
+        _ = torch.randn(1000, device=dev).sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        _, le = model.step(torch.tensor([[tok]], dtype=torch.int32), torch.tensor([pos], dtype=torch.int32),
+                           torch.tensor([0], dtype=torch.int32), caches_e, 64)
+        assert torch.equal(lg, le)
+    for a, b in zip(caches_g, caches_e):
+        assert torch.equal(a, b)
