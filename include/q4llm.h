@@ -41,6 +41,9 @@ enum {
 
 enum { Q4_F32 = 0, Q4_F16 = 1 };
 
+/* prologue codes of q4_gemv_fused */
+enum { Q4_PRO_RMSNORM = 1, Q4_PRO_SWIGLU = 2 };
+
 /* Human-readable text for a status code (static storage). */
 const char* q4llm_status_string(int status);
 /* The hipError_t of the last failed HIP call made by this library on this thread (0 if none). */
@@ -78,6 +81,16 @@ int q4_dequant(const int32_t* qweight, const uint16_t* scales, void* w, int w_dt
  * Requires K % 8 == 0, K % group == 0, group % 8 == 0, K <= 16384, 16-byte aligned qweight/x. */
 int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
             int y_dtype, const float* residual, int64_t N, int64_t K, int group, void* stream);
+
+/* Decode GEMV with the preceding element-wise step fused into its x staging (fp32 x and y):
+ *   Q4_PRO_RMSNORM: x' = rms_norm(x, aux, eps) over K, aux = norm weight [K] (the input /
+ *                   post-attention norms before QLinear, llama_q4.py:141-142, 215-216, 234-235);
+ *   Q4_PRO_SWIGLU:  x holds 2K values (gate | up) and x' = silu(gate) * up (llama_q4.py:236).
+ * then y = residual + W x' exactly as q4_gemv. Needs the vectorised GEMV layout (K % 32 == 0,
+ * group = 32 * 2^j, K <= 8192), otherwise Q4_ERR_UNSUPPORTED. x must not alias y. */
+int q4_gemv_fused(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
+                  const float* aux, float eps, float* y, const float* residual, int64_t N, int64_t K,
+                  int group, void* stream);
 
 /* Prefill projection, replaces QLinear.forward at M > 1 (llama_q4.py:72,
  * F.linear(x, dequantize_q4(W))): y[M, N] = residual + x[M, K] @ dequant(W)^T, x and y fp32.

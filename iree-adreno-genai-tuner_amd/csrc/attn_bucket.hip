@@ -186,46 +186,109 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
   }
   __syncthreads();
 
-  // 5. o = sum_k p[q][k] v[k]: thread owns (query, 8-dim slice) pairs.
-  for (int pr = threadIdx.x; pr < nq * LPK; pr += kThreads) {
-    const int qi = pr / LPK, d8 = pr % LPK;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = 0; k < S; ++k) {
-      const float p = Ps[qi * S + k];
-      float vf[8];
-      unpack8(Vs[k * LPK + d8], vf);
+  // 5. o = sum_k p[q][k] v[k]. Work units are (query, 8-dim slice) pairs; when there are fewer
+  //    pairs than threads the keys of the split are divided among KSPLIT thread groups and the
+  //    group partials are summed through LDS (reusing the score area, no longer needed).
+  const int pairs = nq * LPK;
+  int ksplit = 1;
+  while (ksplit * 2 * pairs <= kThreads && ksplit * 2 <= S / 4) ksplit *= 2;
+  __syncthreads();  // every wave has finished reading P's row statistics above
+  if (ksplit == 1) {
+    for (int pr = threadIdx.x; pr < pairs; pr += kThreads) {
+      const int qi = pr / LPK, d8 = pr % LPK;
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int k = 0; k < S; ++k) {
+        const float p = Ps[qi * S + k];
+        float vf[8];
+        unpack8(Vs[k * LPK + d8], vf);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = fmaf(p, vf[j], acc[j]);
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(p, vf[j], acc[j]);
+      }
+      const int c = c0 + qi / g, h = hk * g + qi % g;
+      float* dst = ws_o + ((static_cast<size_t>(c) * n_q + h) * n_splits + split) * HD + d8 * 8;
+      reinterpret_cast<float4*>(dst)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      reinterpret_cast<float4*>(dst)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     }
-    const int c = c0 + qi / g, h = hk * g + qi % g;
-    float* dst = ws_o + ((static_cast<size_t>(c) * n_q + h) * n_splits + split) * HD + d8 * 8;
-    reinterpret_cast<float4*>(dst)[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    reinterpret_cast<float4*>(dst)[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  } else {
+    float* red = Qs;  // [ksplit][pairs][8] floats; the queries are no longer needed
+    const int pr = threadIdx.x % pairs, ks = threadIdx.x / pairs;
+    if (ks < ksplit) {
+      const int qi = pr / LPK, d8 = pr % LPK;
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int k = ks; k < S; k += ksplit) {
+        const float p = Ps[qi * S + k];
+        float vf[8];
+        unpack8(Vs[k * LPK + d8], vf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(p, vf[j], acc[j]);
+      }
+      float4* r4 = reinterpret_cast<float4*>(red + (ks * pairs + pr) * 8);
+      r4[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      r4[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    __syncthreads();
+    if (threadIdx.x < pairs) {
+      const int qi = threadIdx.x / LPK, d8 = threadIdx.x % LPK;
+      float4 a = make_float4(0, 0, 0, 0), b = make_float4(0, 0, 0, 0);
+      for (int k2 = 0; k2 < ksplit; ++k2) {
+        const float4* r4 = reinterpret_cast<const float4*>(red + (k2 * pairs + threadIdx.x) * 8);
+        a.x += r4[0].x; a.y += r4[0].y; a.z += r4[0].z; a.w += r4[0].w;
+        b.x += r4[1].x; b.y += r4[1].y; b.z += r4[1].z; b.w += r4[1].w;
+      }
+      const int c = c0 + qi / g, h = hk * g + qi % g;
+      float* dst = ws_o + ((static_cast<size_t>(c) * n_q + h) * n_splits + split) * HD + d8 * 8;
+      reinterpret_cast<float4*>(dst)[0] = a;
+      reinterpret_cast<float4*>(dst)[1] = b;
+    }
   }
 }
 
 // Merge the splits of each (row, head): o = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
-// One workgroup of HD threads per (row, head); splits past the row's position are skipped.
+// One workgroup of HD threads per (row, head); splits past the row's position are skipped. The
+// (m, l) pairs are read in parallel (one split per thread, looping when n_splits > HD), the max and
+// the denominator are block reductions, and the o partials are loaded eight splits at a time.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
                                                          float* __restrict__ out, int n_q, int n_splits, int S,
                                                          const int32_t* __restrict__ start_p) {
+  __shared__ float wts[512];
+  __shared__ float red[HD / 64 > 0 ? HD / 64 : 1];
   const int c = blockIdx.x / n_q, h = blockIdx.x % n_q;
   const int d = threadIdx.x;
   const int pos = start_p[0] + c;
-  const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos
+  const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos (n_splits <= 512: host)
   const size_t base = (static_cast<size_t>(c) * n_q + h) * n_splits;
-  float M = -INFINITY;
-  for (int i = 0; i < ns; ++i) M = fmaxf(M, ws_ml[2 * (base + i)]);
-  float num = 0.0f, den = 0.0f;
-  for (int i = 0; i < ns; ++i) {
+  float mloc = -INFINITY;
+  for (int i = d; i < ns; i += HD) mloc = fmaxf(mloc, ws_ml[2 * (base + i)]);
+  mloc = group_max<64>(mloc);
+  if ((d & 63) == 0) red[d >> 6] = mloc;
+  __syncthreads();
+  float M = red[0];
+  for (int w = 1; w < HD / 64; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float den = 0.0f;
+  for (int i = d; i < ns; i += HD) {
     const float m = ws_ml[2 * (base + i)];
-    if (m == -INFINITY) continue;
-    const float w = expf(m - M);
+    const float w = m == -INFINITY ? 0.0f : expf(m - M);
+    wts[i] = w;
     den = fmaf(w, ws_ml[2 * (base + i) + 1], den);
-    num = fmaf(w, ws_o[(base + i) * HD + d], num);
   }
-  out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / den;
+  den = group_sum<64>(den);
+  if ((d & 63) == 0) red[d >> 6] = den;
+  __syncthreads();
+  float D = 0.0f;
+  for (int w = 0; w < HD / 64; ++w) D += red[w];
+  float num = 0.0f;
+  int i = 0;
+  for (; i + 8 <= ns; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ws_o[(base + i + j) * HD + d];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) num = fmaf(wts[i + j], v[j], num);
+  }
+  for (; i < ns; ++i) num = fmaf(wts[i], ws_o[(base + i) * HD + d], num);
+  out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / D;
 }
 
 size_t lds_bytes(int HD, int S) {
@@ -259,6 +322,7 @@ int attn_args(int C, int n_q, int n_kv, int hd, int L) {
   if (n_q % n_kv) return Q4_ERR_SHAPE;
   if (n_q / n_kv > kMaxQ) return Q4_ERR_UNSUPPORTED;
   if (hd != 64 && hd != 128) return Q4_ERR_UNSUPPORTED;
+  if (plan_for(C, n_q, n_kv, L).n_splits > 512) return Q4_ERR_UNSUPPORTED;  // combine holds <= 512 weights
   if (static_cast<int64_t>(L) * n_kv * hd * 2 >= (int64_t{1} << 31)) return Q4_ERR_SHAPE;
   return Q4_OK;
 }

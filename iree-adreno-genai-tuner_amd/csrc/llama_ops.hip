@@ -15,7 +15,8 @@ namespace q4 {
 namespace {
 
 // rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
-// mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w.
+// mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w. Rows of at
+// most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
                                                       const int32_t* __restrict__ row_sel) {
@@ -23,11 +24,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const int64_t row = row_sel ? min(max(static_cast<int64_t>(row_sel[0]), int64_t{0}), M - 1) : blockIdx.x;
   const float* xr = x + row * D;
   float* orow = out + static_cast<int64_t>(blockIdx.x) * D;
+  constexpr int kV = 4;
+  const bool vec = D % 4 == 0 && D <= 4 * 256 * kV;
+  float4 v[kV];
   float s = 0.0f;
-  for (int64_t i = threadIdx.x; i < D; i += 256) {
-    const float v = xr[i];
-    const float sq = v * v;
-    s += sq;
+  if (vec) {
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const int64_t j = threadIdx.x + i * 256;
+      v[i] = j < D / 4 ? reinterpret_cast<const float4*>(xr)[j] : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const float a = v[i].x * v[i].x, b = v[i].y * v[i].y, c = v[i].z * v[i].z, d = v[i].w * v[i].w;
+      s += (a + b) + (c + d);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+      const float t = xr[i];
+      const float sq = t * t;
+      s += sq;
+    }
   }
   s = group_sum<64>(s);
   __shared__ float part[4];
@@ -36,9 +53,21 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const float total = (part[0] + part[1]) + (part[2] + part[3]);
   const float mean = total / static_cast<float>(D);
   const float r = 1.0f / sqrtf(mean + eps);
-  for (int64_t i = threadIdx.x; i < D; i += 256) {
-    const float t = xr[i] * r;
-    orow[i] = t * w[i];
+  if (vec) {
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const int64_t j = threadIdx.x + i * 256;
+      if (j < D / 4) {
+        const float4 ww = reinterpret_cast<const float4*>(w)[j];
+        reinterpret_cast<float4*>(orow)[j] =
+            make_float4((v[i].x * r) * ww.x, (v[i].y * r) * ww.y, (v[i].z * r) * ww.z, (v[i].w * r) * ww.w);
+      }
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+      const float t = xr[i] * r;
+      orow[i] = t * w[i];
+    }
   }
 }
 
@@ -162,6 +191,7 @@ extern "C" int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M
                            const int32_t* row, void* stream) {
   if (!x || !w || !out) return Q4_ERR_NULL;
   if (M <= 0 || D <= 0) return Q4_ERR_SHAPE;
+  if (D % 4 == 0 && (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))) return Q4_ERR_ALIGN;
   const unsigned grid = row ? 1u : static_cast<unsigned>(M);
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row);
   return launch_status();

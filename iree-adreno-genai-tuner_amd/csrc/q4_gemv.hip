@@ -177,6 +177,46 @@ __device__ __forceinline__ void stage_store(const XWords<kF16X, XW>& r, int nwor
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// Fused prologues of the fp32 model path (x is transformed while it is staged):
+//   kProNorm:   x' = rms_norm(x, w, eps) = (x * r) * w, r = 1 / sqrt(mean(x^2) + eps)
+//               (llama_q4.py:141-142; the norm before the qkv and gate/up projections)
+//   kProSwiglu: x holds [gate | up] (2K values), x' = silu(gate) * up (llama_q4.py:236)
+// Every workgroup computes the same r with the same reduction order, so all row blocks see the
+// same x'. Contraction is off in these helpers so each product and sum rounds like the
+// reference's separate tensor ops.
+// ------------------------------------------------------------------------------------------
+constexpr int kProNone = 0, kProNorm = 1, kProSwiglu = 2;
+
+__device__ __forceinline__ float sumsq8(const uint4& a, const uint4& b) {
+#pragma clang fp contract(off)
+  const float4 p = __builtin_bit_cast(float4, a), q = __builtin_bit_cast(float4, b);
+  const float s0 = p.x * p.x, s1 = p.y * p.y, s2 = p.z * p.z, s3 = p.w * p.w;
+  const float s4 = q.x * q.x, s5 = q.y * q.y, s6 = q.z * q.z, s7 = q.w * q.w;
+  return ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7));
+}
+
+__device__ __forceinline__ uint4 norm4(const uint4& xv, const uint4& wv, float r) {
+#pragma clang fp contract(off)
+  const float4 p = __builtin_bit_cast(float4, xv), w = __builtin_bit_cast(float4, wv);
+  const float4 o = make_float4((p.x * r) * w.x, (p.y * r) * w.y, (p.z * r) * w.z, (p.w * r) * w.w);
+  return __builtin_bit_cast(uint4, o);
+}
+
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+#pragma clang fp contract(off)
+  const float e = expf(-g);
+  const float den = 1.0f + e;
+  const float sg = g / den;
+  return sg * u;
+}
+
+__device__ __forceinline__ uint4 swiglu4(const uint4& gv, const uint4& uv) {
+  const float4 g = __builtin_bit_cast(float4, gv), u = __builtin_bit_cast(float4, uv);
+  return __builtin_bit_cast(uint4, make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z),
+                                               silu_mul1(g.w, u.w)));
+}
+
 template <int LPR, int CPL, int R>
 struct Item {
   uint4 w[R][CPL];
@@ -189,10 +229,11 @@ struct Item {
 // so the compute of each chunk starts as soon as that chunk arrives. kMulti == true: a grid-stride
 // loop over items with two register sets (A/B) used alternately, so the next item streams in while
 // the current one is computed and no register copies force early waits.
-template <bool kF16X, bool kF16Y, int LPR, int CPL, int R, int WAVES, int XW, bool kMulti>
+template <bool kF16X, bool kF16Y, int LPR, int CPL, int R, int WAVES, int XW, bool kMulti, int kPro = kProNone>
 __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
-    void* y, const float* residual, int N, int K, int gshift) {
+    void* y, const float* residual, int N, int K, int gshift, const float* __restrict__ aux, float eps) {
+  static_assert(kPro == kProNone || !kF16X, "fused prologues take fp32 x");
   extern __shared__ uint4 smem[];
   constexpr int kRowsPerWave = R * (64 / LPR);
   constexpr int kRows = kRowsPerWave * WAVES;
@@ -208,7 +249,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
 
   const __amdgpu_buffer_rsrc_t wres = make_rsrc(qw, static_cast<uint32_t>(N) * static_cast<uint32_t>(K / 2));
   const __amdgpu_buffer_rsrc_t sres = make_rsrc(scales, static_cast<uint32_t>(N) * spr * 2u);
-  const __amdgpu_buffer_rsrc_t xres = make_rsrc(x, static_cast<uint32_t>(K) * (kF16X ? 2u : 4u));
+  const __amdgpu_buffer_rsrc_t xres =
+      make_rsrc(x, static_cast<uint32_t>(K) * (kF16X ? 2u : 4u) * (kPro == kProSwiglu ? 2u : 1u));
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -278,8 +320,42 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
 
   XWords<kF16X, XW> xr;
   stage_load<kF16X, XW>(xres, xr);
+  XWords<kF16X, XW> ar;  // second operand of the prologue: norm weights, or the `up` half
+  if constexpr (kPro == kProNorm) stage_load<kF16X, XW>(make_rsrc(aux, static_cast<uint32_t>(K) * 4u), ar);
+  if constexpr (kPro == kProSwiglu) {
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      const uint32_t wd = threadIdx.x + i * blockDim.x;
+      ar.v[2 * i] = buf_load16(xres, static_cast<uint32_t>(K) * 4u + wd * 32u);
+      ar.v[2 * i + 1] = buf_load16(xres, static_cast<uint32_t>(K) * 4u + wd * 32u + 16u);
+    }
+  }
   Item<LPR, CPL, R> a;
   load_item(0, a);  // a workgroup without items gets rows past N: out of range, no traffic
+  if constexpr (kPro == kProNorm) {
+    // words past K loaded as zeros, so they add nothing to the sum of squares
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XW; ++i) ss += sumsq8(xr.v[2 * i], xr.v[2 * i + 1]);
+    ss = group_sum<64>(ss);
+    __shared__ float red[WAVES];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) total += red[w];
+    const float mean = total / static_cast<float>(K);
+    const float r = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      xr.v[2 * i] = norm4(xr.v[2 * i], ar.v[2 * i], r);
+      xr.v[2 * i + 1] = norm4(xr.v[2 * i + 1], ar.v[2 * i + 1], r);
+    }
+  }
+  if constexpr (kPro == kProSwiglu) {
+#pragma unroll
+    for (int i = 0; i < 2 * XW; ++i) xr.v[i] = swiglu4(xr.v[i], ar.v[i]);
+  }
   if constexpr (!kMulti) {
     stage_store<kF16X, XW>(xr, nwords, cpr, xs, corr_w, junk);
     __syncthreads();
@@ -307,7 +383,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
 template <bool kF16X, bool kF16Y>
 __global__ __launch_bounds__(256) void q4_gemv_generic(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
-    void* y, const float* residual, int N, int K, int group) {
+    void* y, const float* residual, int N, int K, int group, const float*, float) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= N) return;
@@ -371,24 +447,27 @@ constexpr Cfg kCfgs[] = {
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <bool F16X, bool F16Y, int I>
+template <bool F16X, bool F16Y, int I, int PRO>
 struct KernelOf {
   static constexpr Cfg c = kCfgs[I];
-  static constexpr auto fn = q4_gemv_kernel<F16X, F16Y, c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi>;
+  static constexpr auto fn = q4_gemv_kernel<F16X, F16Y, c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi, PRO>;
 };
 
-// last argument: the generic kernel takes the group size, the vectorised kernel log2(group / 32)
-using KernelFn = void (*)(const int32_t*, const uint16_t*, const void*, void*, const float*, int, int, int);
+// group argument: the generic kernel takes the group size, the vectorised kernel log2(group / 32)
+using KernelFn = void (*)(const int32_t*, const uint16_t*, const void*, void*, const float*, int, int, int,
+                          const float*, float);
 
-template <bool F16X, bool F16Y, int... Is>
+template <bool F16X, bool F16Y, int PRO, int... Is>
 constexpr auto make_table(std::integer_sequence<int, Is...>) {
-  return std::array<KernelFn, sizeof...(Is)>{KernelOf<F16X, F16Y, Is>::fn...};
+  return std::array<KernelFn, sizeof...(Is)>{KernelOf<F16X, F16Y, Is, PRO>::fn...};
 }
 
-const auto kTabF32F32 = make_table<false, false>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF32F16 = make_table<false, true>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF16F32 = make_table<true, false>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF16F16 = make_table<true, true>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF32F32 = make_table<false, false, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF32F16 = make_table<false, true, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF16F32 = make_table<true, false, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabF16F16 = make_table<true, true, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabNorm = make_table<false, false, kProNorm>(std::make_integer_sequence<int, kNumCfgs>{});
+const auto kTabSwiglu = make_table<false, false, kProSwiglu>(std::make_integer_sequence<int, kNumCfgs>{});
 
 int rows_per_block(const Cfg& c) { return c.r * (64 / c.lpr) * c.waves; }
 
@@ -447,7 +526,8 @@ int set_lds_limit(KernelFn fn, size_t bytes) {
 // Runs config `cfg` (-1 = automatic choice) with `grid_override` workgroups (0 = automatic).
 int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
                    int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg,
-                   int grid_override, hipStream_t stream) {
+                   int grid_override, hipStream_t stream, int prologue = kProNone, const float* aux = nullptr,
+                   float eps = 0.0f) {
   const bool f16x = x_dtype == Q4_F16, f16y = y_dtype == Q4_F16;
   int ci = cfg >= 0 && cfg < kNumCfgs ? cfg : choose_cfg(N, K, f16x);
   if (!cfg_fits(kCfgs[ci], N, K)) ci = 22;
@@ -460,15 +540,18 @@ int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x
   const bool vec = (K % 32 == 0) && pow2_group && K <= kMaxK && cfg_fits(c, N, K) &&
                    N * (K / 2) < (int64_t{1} << 31) && max_row * (K / 2) < (int64_t{1} << 32) &&
                    aligned(qweight, 16) && aligned(x, 16);
+  if (!vec && prologue != kProNone) return Q4_ERR_UNSUPPORTED;
   if (!vec) {
     const dim3 grid(static_cast<unsigned>((N + 3) / 4)), block(256);
-    if (f16x && f16y) hipLaunchKernelGGL((q4_gemv_generic<true, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
-    else if (f16x) hipLaunchKernelGGL((q4_gemv_generic<true, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
-    else if (f16y) hipLaunchKernelGGL((q4_gemv_generic<false, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
-    else hipLaunchKernelGGL((q4_gemv_generic<false, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group);
+    if (f16x && f16y) hipLaunchKernelGGL((q4_gemv_generic<true, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
+    else if (f16x) hipLaunchKernelGGL((q4_gemv_generic<true, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
+    else if (f16y) hipLaunchKernelGGL((q4_gemv_generic<false, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
+    else hipLaunchKernelGGL((q4_gemv_generic<false, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
     return launch_status();
   }
   KernelFn fn = f16x ? (f16y ? kTabF16F16[ci] : kTabF16F32[ci]) : (f16y ? kTabF32F16[ci] : kTabF32F32[ci]);
+  if (prologue == kProNorm) fn = kTabNorm[ci];
+  if (prologue == kProSwiglu) fn = kTabSwiglu[ci];
   const size_t lds = f16x ? lds_bytes<true>(K) : lds_bytes<false>(K);
   if (int st = set_lds_limit(fn, lds)) return st;
   const int64_t blocks = (N + rows_per_block(c) - 1) / rows_per_block(c);
@@ -480,7 +563,7 @@ int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x
     if (grid_override > 0) grid = grid_override < blocks ? grid_override : blocks;
   }
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(threads), lds, stream, qweight, scales, x, y,
-                     residual, (int)N, (int)K, __builtin_ctz(gchunks));
+                     residual, (int)N, (int)K, __builtin_ctz(gchunks), aux, eps);
   return launch_status();
 }
 
@@ -518,3 +601,16 @@ extern "C" int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const
 }
 
 extern "C" int q4_gemv_num_configs(void) { return q4::q4_gemv_num_cfgs(); }
+
+extern "C" int q4_gemv_fused(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
+                             const float* aux, float eps, float* y, const float* residual, int64_t N, int64_t K,
+                             int group, void* stream) {
+  if (int st = gemv_args(qweight, scales, x, Q4_F32, y, Q4_F32, residual, N, K, group)) return st;
+  if (prologue != Q4_PRO_RMSNORM && prologue != Q4_PRO_SWIGLU) return Q4_ERR_DTYPE;
+  if (prologue == Q4_PRO_RMSNORM && !aux) return Q4_ERR_NULL;
+  if (prologue == Q4_PRO_RMSNORM && !q4::aligned(aux, 16)) return Q4_ERR_ALIGN;
+  // other workgroups may still be staging x while y is written, so x must not alias y
+  if (static_cast<const void*>(x) == static_cast<const void*>(y)) return Q4_ERR_SHAPE;
+  return q4::q4_gemv_launch(qweight, scales, x, Q4_F32, y, Q4_F32, residual, N, K, group, -1, 0,
+                            q4::as_stream(stream), prologue, aux, eps);
+}

@@ -75,6 +75,13 @@ int proj(int C, const float* x, const int32_t* q, const uint16_t* s, float* y, c
   return q4_linear(x, C, q, s, y, res, N, K, group, stream);
 }
 
+// The fused GEMV prologues need the vectorised layout: K % 32 == 0, group = 32 * 2^j, K <= 8192.
+bool gemv_fusable(int D, int inter, int group) {
+  const int gc = group / 32;
+  const bool pow2 = group % 32 == 0 && gc > 0 && (gc & (gc - 1)) == 0;
+  return pow2 && D % 32 == 0 && inter % 32 == 0 && D <= 8192 && inter <= 8192;
+}
+
 }  // namespace
 
 extern "C" int q4llm_step_workspace_bytes(const q4llm_model* m, int C, int L, size_t* bytes) {
@@ -119,20 +126,35 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
     if (st_ != Q4_OK) return st_; \
   } while (0)
 
+  // Decode (C == 1) uses the GEMVs with fused norm / SwiGLU prologues when the shapes take the
+  // vectorised GEMV (true for every BASELINE model); prefill uses the separate kernels.
+  const bool fused = C == 1 && gemv_fusable(D, m->inter, m->group);
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
     uint16_t* kc = static_cast<uint16_t*>(caches[2 * i]);
     uint16_t* vc = static_cast<uint16_t*>(caches[2 * i + 1]);
-    Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
-    Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, stream));
+    if (fused) {  // decode: norms and SwiGLU run inside the GEMVs' x staging
+      Q4_TRY(q4_gemv_fused(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, qkv, nullptr, qkv_w, D,
+                           m->group, stream));
+    } else {
+      Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
+      Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, stream));
+    }
     Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
     Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, stream));
-    Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
-    Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, stream));
-    Q4_TRY(silu_mul_f32(gu, act, C, m->inter, stream));
-    Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, stream));
+    if (fused) {
+      Q4_TRY(q4_gemv_fused(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, gu, nullptr, 2 * m->inter, D,
+                           m->group, stream));
+      Q4_TRY(q4_gemv_fused(ly.wdown_q, ly.wdown_s, gu, Q4_PRO_SWIGLU, nullptr, 0.0f, h, h, D, m->inter, m->group,
+                           stream));
+    } else {
+      Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
+      Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, stream));
+      Q4_TRY(silu_mul_f32(gu, act, C, m->inter, stream));
+      Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, stream));
+    }
   }
   Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
   Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));

@@ -88,6 +88,38 @@ class SyntheticWeights:
             return dict(zip(names, ex.map(self.__getitem__, names)))
 
 
+class PrefetchingWeights(SyntheticWeights):
+    """SyntheticWeights whose tensors are generated ahead of use by a thread pool, in state-dict
+    order, keeping at most `lookahead` generated tensors in memory. Values are identical to
+    SyntheticWeights (each tensor has its own stream)."""
+
+    def __init__(self, cfg, seed=0, std=0.02, workers=None, lookahead=24):
+        super().__init__(cfg, seed, std)
+        self.order = [name for name, _, _ in tensor_specs(cfg)]
+        self.workers = workers or min(16, os.cpu_count() or 1)
+        self.lookahead = lookahead
+        self._ex = cf.ThreadPoolExecutor(self.workers)
+        self._fut = {}
+        self._next = 0
+        self._fill()
+
+    def _fill(self):
+        while self._next < len(self.order) and len(self._fut) < self.lookahead:
+            name = self.order[self._next]
+            self._fut[name] = self._ex.submit(SyntheticWeights.__getitem__, self, name)
+            self._next += 1
+
+    def __getitem__(self, k):
+        f = self._fut.pop(k, None)
+        out = f.result() if f is not None else SyntheticWeights.__getitem__(self, k)
+        self._fill()
+        return out
+
+    def close(self):
+        self._ex.shutdown(wait=False, cancel_futures=True)
+        self._fut.clear()
+
+
 def pack_nibbles(nib: np.ndarray) -> np.ndarray:
     """[N, K] nibbles in [0, 15] -> [N, K/8] int32, nibble b of word j = k 8j + b (llama_q4.py:27-37)."""
     n, k = nib.shape

@@ -122,3 +122,39 @@ def test_gemv_all_configs_agree(dev):
             ops.q4_gemv_cfg(qd, sd_, xd, 128, y, cfg=cfg, grid=grid)
             err = (y.cpu().double() - ref).abs().max().item()
             assert err <= 1e-2 * rms, (cfg, grid, err)
+
+
+@pytest.mark.parametrize("n,k,group", [(5120, 3072, 128), (16384, 3072, 128), (512, 256, 32), (1408, 256, 32)])
+def test_gemv_fused_rmsnorm(dev, n, k, group):
+    """q4_gemv_fused(RMSNORM): y = W rms_norm(x, w, eps) + residual (llama_q4.py:141-142, 215-216)."""
+    from q4llm._lib import LIB, ptr, stream_of
+    g = torch.Generator().manual_seed(n + k + 1)
+    wq = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(wq, group)
+    h = torch.randn(k, generator=g) * 3
+    lnw = torch.rand(k, generator=g) + 0.5
+    xn = R.rms_norm(h[None], lnw, 1e-5)[0]
+    ref = R.dequantize_q4(qw, sc, group).double() @ xn.double()
+    rms = ref.pow(2).mean().sqrt().item()
+    y = torch.full((n,), float("nan"), device=dev)
+    qd, sd_, hd, lw = qw.to(dev), sc.to(dev), h.to(dev), lnw.to(dev)  # keep the device tensors alive
+    LIB.call("q4_gemv_fused", ptr(qd), ptr(sd_), ptr(hd), 1, ptr(lw), 1e-5, ptr(y), None, n, k, group, stream_of(dev))
+    assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+
+
+@pytest.mark.parametrize("n,k,group", [(3072, 8192, 128), (256, 704, 32)])
+def test_gemv_fused_swiglu_residual(dev, n, k, group):
+    """q4_gemv_fused(SWIGLU): h = h + W (silu(gate) * up) (llama_q4.py:236)."""
+    from q4llm._lib import LIB, ptr, stream_of
+    g = torch.Generator().manual_seed(n + k + 2)
+    wq = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(wq, group)
+    gu = torch.randn(2 * k, generator=g) * 2
+    res = torch.randn(n, generator=g)
+    act = torch.nn.functional.silu(gu[:k]) * gu[k:]
+    ref = R.dequantize_q4(qw, sc, group).double() @ act.double() + res.double()
+    rms = ref.pow(2).mean().sqrt().item()
+    hd = res.to(dev).clone()
+    qd, sd_, gud = qw.to(dev), sc.to(dev), gu.to(dev)  # keep the device tensors alive
+    LIB.call("q4_gemv_fused", ptr(qd), ptr(sd_), ptr(gud), 2, None, 0.0, ptr(hd), ptr(hd), n, k, group, stream_of(dev))
+    assert (hd.cpu().double() - ref).abs().max().item() <= 1e-5 * rms

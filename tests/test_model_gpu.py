@@ -106,3 +106,18 @@ def test_graph_replay_matches_eager_step(dev):
         assert torch.equal(lg, le)
     for a, b in zip(caches_g, caches_e):
         assert torch.equal(a, b)
+
+
+def test_llama32_3b_generation_matches_golden(dev):
+    """Llama-3.2-3B shape, synthetic N(0, 0.02) int4 weights (group 128), 512-token
+    prompt prefilled in chunks of 256, 256 greedy tokens over buckets 256..4096: the token ids
+    equal the CPU oracle's (tests/golden/make_golden.py 3b) exactly."""
+    gold = json.loads((GOLD / "llama32_3b_tokens.json").read_text())
+    sd = synth.PrefetchingWeights(synth.LLAMA32_3B, gold["seed"])
+    model = LlamaQ4(None, group=gold["group"], max_ctx=gold["max_ctx"], sd=sd, cfg=synth.LLAMA32_3B)
+    sd.close()
+    res = llm_runner.run(model, gold["prompt"], gold["max_new_tokens"], gold["chunk"], gold["buckets"])
+    assert [L for L, _ in res["chunks"]] == [256, 512]
+    assert res["tokens"] == gold["tokens"]
+    del model
+    torch.cuda.empty_cache()
