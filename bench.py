@@ -36,6 +36,12 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 2 ** 20
 
+# HBM bytes per 5120x3072 launch from rocprofv3 counter passes over this bench's GEMV leg
+# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4023.0 KiB x 1.995 (the factor that maps
+# FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 20.0 KiB x 1.0.
+# Counters cannot be read inside a timed run, so the figure is carried here with its source.
+GEMV_TRAFFIC_BYTES_5120x3072 = 8_238_986
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -365,7 +371,8 @@ def main():
         "config": {"workload": "int4 decode GEMV y=Wx, N=5120 (fused qkv), K=3072, group 128, batch 1",
                    "N": 5120, "K": 3072, "group": 128, "weight_copies_rotated": 64},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES_5120x3072,
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
                      "algorithmic_bytes_per_launch": head["bytes"], "avg_launch_us": round(head["us"], 4),
                      "measured_read_floor_us_same_bytes": floor,
                      "frac_of_measured_read_floor": round(floor / head["us"], 4)},
