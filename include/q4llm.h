@@ -41,8 +41,11 @@ enum {
 
 enum { Q4_F32 = 0, Q4_F16 = 1 };
 
-/* prologue codes of q4_gemv_fused */
-enum { Q4_PRO_RMSNORM = 1, Q4_PRO_SWIGLU = 2 };
+/* prologue codes of q4_gemv_fused / q4_gemv_epilogue */
+enum { Q4_PRO_NONE = 0, Q4_PRO_RMSNORM = 1, Q4_PRO_SWIGLU = 2 };
+
+/* epilogue codes of q4_gemv_epilogue */
+enum { Q4_EPI_SWIGLU = 1, Q4_EPI_ROPE_KV = 2 };
 
 /* Human-readable text for a status code (static storage). */
 const char* q4llm_status_string(int status);
@@ -87,10 +90,38 @@ int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x
  *                   post-attention norms before QLinear, llama_q4.py:141-142, 215-216, 234-235);
  *   Q4_PRO_SWIGLU:  x holds 2K values (gate | up) and x' = silu(gate) * up (llama_q4.py:236).
  * then y = residual + W x' exactly as q4_gemv. Needs the vectorised GEMV layout (K % 32 == 0,
- * group = 32 * 2^j, K <= 8192), otherwise Q4_ERR_UNSUPPORTED. x must not alias y. */
+ * group = 32 * 2^j, K <= 8192), otherwise Q4_ERR_UNSUPPORTED. x must not alias y.
+ * The rms_norm form stages x * aux and scales each finished row by r = 1 / sqrt(mean(x^2) + eps):
+ * W ((x * r) * aux) up to fp32 rounding. */
 int q4_gemv_fused(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
                   const float* aux, float eps, float* y, const float* residual, int64_t N, int64_t K,
                   int group, void* stream);
+
+/* RoPE tables and KV caches of the Q4_EPI_ROPE_KV epilogue: cos_t / sin_t [max_ctx, head_dim]
+ * fp32 (llama_q4.py:184-192), k_cache / v_cache fp16 [max_ctx, n_kv, head_dim], start: device
+ * int32 [1] holding the position of the token. */
+typedef struct q4_rope_kv {
+  const float* cos_t;
+  const float* sin_t;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const int32_t* start;
+  int n_q, n_kv, head_dim, max_ctx;
+} q4_rope_kv;
+
+/* Decode GEMV whose rows are finished in pairs by the step that follows the projection in
+ * LlamaQ4.step (fp32 x and y, optional Q4_PRO_RMSNORM prologue as in q4_gemv_fused):
+ *   Q4_EPI_SWIGLU:  W is the fused [gate | up] weight (N = 2 * inter); y[i] = silu(g_i) * u_i
+ *                   with g = W[:inter] x', u = W[inter:] x' (llama_q4.py:236); y has inter values.
+ *   Q4_EPI_ROPE_KV: W is the fused [q | k | v] weight (N = (n_q + 2 n_kv) * head_dim); y = qkv
+ *                   with q and k rotated at pos = start[0] (llama_q4.py:205-207, 218-221), and the
+ *                   k and v rows written as fp16 to k_cache / v_cache at row pos (llama_q4.py:
+ *                   222-223). pos outside [0, max_ctx) leaves y unrotated and the caches untouched.
+ * Replaces the q4_gemv + silu_mul_f32 and q4_gemv + rope_kv_write pairs of one decode token.
+ * Same layout requirements as q4_gemv_fused; N even. x must not alias y. */
+int q4_gemv_epilogue(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
+                     const float* aux, float eps, int epilogue, const q4_rope_kv* rope, float* y, int64_t N,
+                     int64_t K, int group, void* stream);
 
 /* Prefill projection, replaces QLinear.forward at M > 1 (llama_q4.py:72,
  * F.linear(x, dequantize_q4(W))): y[M, N] = residual + x[M, K] @ dequant(W)^T, x and y fp32.

@@ -196,11 +196,9 @@ __device__ __forceinline__ float sumsq8(const uint4& a, const uint4& b) {
   return ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7));
 }
 
-__device__ __forceinline__ uint4 norm4(const uint4& xv, const uint4& wv, float r) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ uint4 mul4(const uint4& xv, const uint4& wv) {
   const float4 p = __builtin_bit_cast(float4, xv), w = __builtin_bit_cast(float4, wv);
-  const float4 o = make_float4((p.x * r) * w.x, (p.y * r) * w.y, (p.z * r) * w.z, (p.w * r) * w.w);
-  return __builtin_bit_cast(uint4, o);
+  return __builtin_bit_cast(uint4, make_float4(p.x * w.x, p.y * w.y, p.z * w.z, p.w * w.w));
 }
 
 __device__ __forceinline__ float silu_mul1(float g, float u) {
@@ -217,6 +215,38 @@ __device__ __forceinline__ uint4 swiglu4(const uint4& gv, const uint4& uv) {
                                                silu_mul1(g.w, u.w)));
 }
 
+// ------------------------------------------------------------------------------------------
+// Paired-row epilogues of the decode step (R == 2: a lane's two rows form a pair p):
+//   kEpiSwiglu: rows p and p + N/2 (gate and up of the fused [gate | up] weight);
+//               y[p] = silu(gate) * up, y has N/2 values (llama_q4.py:236).
+//   kEpiRope:   rows (head, d) and (head, d + hd/2) of the fused [q | k | v] weight; q and k are
+//               rotated at pos = start[0] (x * cos + rotate_half(x) * sin, llama_q4.py:205-207,
+//               218-221) and written to y; k and v are also written to the fp16 caches at row pos
+//               (llama_q4.py:222-223). pos outside [0, max_ctx) leaves y unrotated and the caches
+//               untouched.
+// ------------------------------------------------------------------------------------------
+constexpr int kEpiNone = 0, kEpiSwiglu = 1, kEpiRope = 2;
+
+struct EpiArgs {
+  const float* cos_t;
+  const float* sin_t;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int32_t* start;
+  int n_q, n_kv, hd, max_ctx;
+};
+
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1, float c2, float s2, float& lo,
+                                          float& hi) {
+#pragma clang fp contract(off)
+  const float a = x1 * c1;
+  const float b = (-x2) * s1;
+  lo = a + b;
+  const float e = x2 * c2;
+  const float f = x1 * s2;
+  hi = e + f;
+}
+
 template <int LPR, int CPL, int R>
 struct Item {
   uint4 w[R][CPL];
@@ -229,11 +259,15 @@ struct Item {
 // so the compute of each chunk starts as soon as that chunk arrives. kMulti == true: a grid-stride
 // loop over items with two register sets (A/B) used alternately, so the next item streams in while
 // the current one is computed and no register copies force early waits.
-template <bool kF16X, bool kF16Y, int LPR, int CPL, int R, int WAVES, int XW, bool kMulti, int kPro = kProNone>
+template <bool kF16X, bool kF16Y, int LPR, int CPL, int R, int WAVES, int XW, bool kMulti, int kPro = kProNone,
+          int kEpi = kEpiNone>
 __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
-    void* y, const float* residual, int N, int K, int gshift, const float* __restrict__ aux, float eps) {
+    void* y, const float* residual, int N, int K, int gshift, const float* __restrict__ aux, float eps,
+    EpiArgs ea) {
   static_assert(kPro == kProNone || !kF16X, "fused prologues take fp32 x");
+  static_assert(kEpi == kEpiNone || (R == 2 && !kF16X && !kF16Y), "paired epilogues take fp32 x/y, R == 2");
+  __shared__ float red[WAVES];  // per-wave sums of squares of the rms_norm prologue
   extern __shared__ uint4 smem[];
   constexpr int kRowsPerWave = R * (64 / LPR);
   constexpr int kRows = kRowsPerWave * WAVES;
@@ -262,6 +296,23 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
   auto item_row0 = [&](int it) {
     return (blockIdx.x + (it / n_kpass) * gridDim.x) * kRows + wave * kRowsPerWave + rg * R;
   };
+  // Weight row of virtual row v: v itself, or for the paired epilogues row b = v & 1 of pair
+  // p = v >> 1; pairs past N/2 map to row N (out of range: zeros, no traffic).
+  auto phys_row = [&](int v) -> int {
+    if constexpr (kEpi == kEpiNone) {
+      return v;
+    } else {
+      const int pr = v >> 1, b = v & 1;
+      if (pr >= (N >> 1)) return N;
+      if constexpr (kEpi == kEpiSwiglu) {
+        return pr + b * (N >> 1);
+      } else {
+        const int hh = ea.hd >> 1;
+        const int head = pr / hh;
+        return head * ea.hd + (pr - head * hh) + b * hh;
+      }
+    }
+  };
   // Loads of one item. Rows past N fall outside the buffer resource by themselves; chunks past
   // the row get kOOB; both return zeros without memory traffic, so no branches are needed.
   auto load_item = [&](int it, Item<LPR, CPL, R>& d) {
@@ -269,7 +320,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
     const int row0 = item_row0(it);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t row = static_cast<uint32_t>(row0 + r);
+      const uint32_t row = static_cast<uint32_t>(phys_row(row0 + r));
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = kp * (LPR * CPL) + i * LPR + lr;
@@ -283,6 +334,40 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  float rnorm = 1.0f;  // rms_norm scale, applied to the finished rows
+  auto epilogue_pair = [&](int pr, float ya, float yb) {
+    float* yf = reinterpret_cast<float*>(y);
+    if constexpr (kEpi == kEpiSwiglu) {
+      yf[pr] = silu_mul1(ya, yb);
+    } else {
+      const int hd = ea.hd, hh = hd >> 1;
+      const int head = pr / hh, d = pr - head * hh;
+      const int ra = head * hd + d;
+      const int pos = ea.start[0];
+      if (pos < 0 || pos >= ea.max_ctx) {
+        yf[ra] = ya;
+        yf[ra + hh] = yb;
+      } else if (head < ea.n_q + ea.n_kv) {
+        const float* cp = ea.cos_t + static_cast<int64_t>(pos) * hd;
+        const float* sp = ea.sin_t + static_cast<int64_t>(pos) * hd;
+        float lo, hi;
+        rope_pair(ya, yb, cp[d], sp[d], cp[d + hh], sp[d + hh], lo, hi);
+        yf[ra] = lo;
+        yf[ra + hh] = hi;
+        if (head >= ea.n_q) {
+          uint16_t* dst = ea.kc + (static_cast<int64_t>(pos) * ea.n_kv + (head - ea.n_q)) * hd;
+          dst[d] = float_to_half_bits(lo);
+          dst[d + hh] = float_to_half_bits(hi);
+        }
+      } else {
+        yf[ra] = ya;
+        yf[ra + hh] = yb;
+        uint16_t* dst = ea.vc + (static_cast<int64_t>(pos) * ea.n_kv + (head - ea.n_q - ea.n_kv)) * hd;
+        dst[d] = float_to_half_bits(ya);
+        dst[d + hh] = float_to_half_bits(yb);
+      }
+    }
+  };
   // Accumulate one item; on the last K pass reduce over the LPR lanes and store.
   auto compute_item = [&](int it, const Item<LPR, CPL, R>& d) {
     const int kp = it % n_kpass;
@@ -302,18 +387,28 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
     }
     if (kp == n_kpass - 1) {
       const int row0 = item_row0(it);
+      float v[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float v = segment_sum_to_last<LPR>(acc[r]);
+        v[r] = segment_sum_to_last<LPR>(acc[r]);
+        if constexpr (kPro == kProNorm) v[r] *= rnorm;
         acc[r] = 0.0f;
-        const int row = row0 + r;
-        if (lr == LPR - 1 && row < N) {
-          if constexpr (kF16Y) {
-            reinterpret_cast<uint16_t*>(y)[row] = float_to_half_bits(v);
-          } else {
-            reinterpret_cast<float*>(y)[row] = residual ? residual[row] + v : v;
+      }
+      if constexpr (kEpi == kEpiNone) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = row0 + r;
+          if (lr == LPR - 1 && row < N) {
+            if constexpr (kF16Y) {
+              reinterpret_cast<uint16_t*>(y)[row] = float_to_half_bits(v[r]);
+            } else {
+              reinterpret_cast<float*>(y)[row] = residual ? residual[row] + v[r] : v[r];
+            }
           }
         }
+      } else {
+        const int pr = row0 >> 1;
+        if (lr == LPR - 1 && pr < (N >> 1)) epilogue_pair(pr, v[0], v[1]);
       }
     }
   };
@@ -333,25 +428,28 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
   Item<LPR, CPL, R> a;
   load_item(0, a);  // a workgroup without items gets rows past N: out of range, no traffic
   if constexpr (kPro == kProNorm) {
-    // words past K loaded as zeros, so they add nothing to the sum of squares
+    // Sum of squares for r = 1 / sqrt(mean(x^2) + eps); x * w is staged and the finished rows
+    // are scaled by r, so the reduction shares the staging barrier. Words past K load as zeros.
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < XW; ++i) ss += sumsq8(xr.v[2 * i], xr.v[2 * i + 1]);
     ss = group_sum<64>(ss);
-    __shared__ float red[WAVES];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) total += red[w];
-    const float mean = total / static_cast<float>(K);
-    const float r = 1.0f / sqrtf(mean + eps);
 #pragma unroll
     for (int i = 0; i < XW; ++i) {
-      xr.v[2 * i] = norm4(xr.v[2 * i], ar.v[2 * i], r);
-      xr.v[2 * i + 1] = norm4(xr.v[2 * i + 1], ar.v[2 * i + 1], r);
+      xr.v[2 * i] = mul4(xr.v[2 * i], ar.v[2 * i]);
+      xr.v[2 * i + 1] = mul4(xr.v[2 * i + 1], ar.v[2 * i + 1]);
     }
   }
+  auto norm_scale = [&]() {
+    if constexpr (kPro == kProNorm) {
+      float total = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) total += red[w];
+      const float mean = total / static_cast<float>(K);
+      rnorm = 1.0f / sqrtf(mean + eps);
+    }
+  };
   if constexpr (kPro == kProSwiglu) {
 #pragma unroll
     for (int i = 0; i < 2 * XW; ++i) xr.v[i] = swiglu4(xr.v[i], ar.v[i]);
@@ -359,12 +457,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
   if constexpr (!kMulti) {
     stage_store<kF16X, XW>(xr, nwords, cpr, xs, corr_w, junk);
     __syncthreads();
+    norm_scale();
     compute_item(0, a);
   } else {
     Item<LPR, CPL, R> b;
     load_item(1, b);
     stage_store<kF16X, XW>(xr, nwords, cpr, xs, corr_w, junk);
     __syncthreads();
+    norm_scale();
     const int my_blocks = static_cast<int>(blockIdx.x) < n_blocks ? (n_blocks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
     const int n_items = my_blocks * n_kpass;
     // items past the end are out-of-range loads (zeros) whose rows lie past N, so computing them
@@ -383,7 +483,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
 template <bool kF16X, bool kF16Y>
 __global__ __launch_bounds__(256) void q4_gemv_generic(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const void* __restrict__ x,
-    void* y, const float* residual, int N, int K, int group, const float*, float) {
+    void* y, const float* residual, int N, int K, int group, const float*, float, EpiArgs) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= N) return;
@@ -447,27 +547,37 @@ constexpr Cfg kCfgs[] = {
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <bool F16X, bool F16Y, int I, int PRO>
-struct KernelOf {
-  static constexpr Cfg c = kCfgs[I];
-  static constexpr auto fn = q4_gemv_kernel<F16X, F16Y, c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi, PRO>;
-};
-
 // group argument: the generic kernel takes the group size, the vectorised kernel log2(group / 32)
 using KernelFn = void (*)(const int32_t*, const uint16_t*, const void*, void*, const float*, int, int, int,
-                          const float*, float);
+                          const float*, float, EpiArgs);
 
-template <bool F16X, bool F16Y, int PRO, int... Is>
-constexpr auto make_table(std::integer_sequence<int, Is...>) {
-  return std::array<KernelFn, sizeof...(Is)>{KernelOf<F16X, F16Y, Is, PRO>::fn...};
+// Paired epilogues exist only for the two-rows-per-lane entries (nullptr elsewhere).
+template <bool F16X, bool F16Y, int I, int PRO, int EPI>
+constexpr KernelFn kernel_of() {
+  constexpr Cfg c = kCfgs[I];
+  if constexpr (EPI != kEpiNone && c.r != 2) {
+    return nullptr;
+  } else {
+    return q4_gemv_kernel<F16X, F16Y, c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi, PRO, EPI>;
+  }
 }
 
-const auto kTabF32F32 = make_table<false, false, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF32F16 = make_table<false, true, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF16F32 = make_table<true, false, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabF16F16 = make_table<true, true, kProNone>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabNorm = make_table<false, false, kProNorm>(std::make_integer_sequence<int, kNumCfgs>{});
-const auto kTabSwiglu = make_table<false, false, kProSwiglu>(std::make_integer_sequence<int, kNumCfgs>{});
+template <bool F16X, bool F16Y, int PRO, int EPI, int... Is>
+constexpr auto make_table(std::integer_sequence<int, Is...>) {
+  return std::array<KernelFn, sizeof...(Is)>{kernel_of<F16X, F16Y, Is, PRO, EPI>()...};
+}
+
+using Seq = std::make_integer_sequence<int, kNumCfgs>;
+const auto kTabF32F32 = make_table<false, false, kProNone, kEpiNone>(Seq{});
+const auto kTabF32F16 = make_table<false, true, kProNone, kEpiNone>(Seq{});
+const auto kTabF16F32 = make_table<true, false, kProNone, kEpiNone>(Seq{});
+const auto kTabF16F16 = make_table<true, true, kProNone, kEpiNone>(Seq{});
+const auto kTabNorm = make_table<false, false, kProNorm, kEpiNone>(Seq{});
+const auto kTabSwiglu = make_table<false, false, kProSwiglu, kEpiNone>(Seq{});
+const auto kTabEpiSwiglu = make_table<false, false, kProNone, kEpiSwiglu>(Seq{});
+const auto kTabEpiRope = make_table<false, false, kProNone, kEpiRope>(Seq{});
+const auto kTabNormEpiSwiglu = make_table<false, false, kProNorm, kEpiSwiglu>(Seq{});
+const auto kTabNormEpiRope = make_table<false, false, kProNorm, kEpiRope>(Seq{});
 
 int rows_per_block(const Cfg& c) { return c.r * (64 / c.lpr) * c.waves; }
 
@@ -481,27 +591,33 @@ bool cfg_fits(const Cfg& c, int64_t N, int64_t K) {
 
 // Fixed rule: measured entries for the shapes of the 3B model and the benchmark; otherwise the
 // fitting single-item entry with the least padding in K and rows and the most even spread of
-// workgroups over 256 CUs, or the grid-stride entry when no single-item entry fits.
-int choose_cfg(int64_t N, int64_t K, bool f16x) {
+// workgroups over 256 CUs, or the grid-stride entry when no single-item entry fits. `paired`
+// (the paired-row epilogues) restricts the choice to single-item entries with two rows per lane.
+int choose_cfg(int64_t N, int64_t K, bool paired) {
+  auto usable = [&](int i) { return cfg_fits(kCfgs[i], N, K) && (!paired || (kCfgs[i].r == 2 && !kCfgs[i].multi)); };
   const char* ov = getenv("Q4_GEMV_CFG");
   if (ov && *ov) {
     const int i = atoi(ov);
-    if (i >= 0 && i < kNumCfgs && cfg_fits(kCfgs[i], N, K)) return i;
+    if (i >= 0 && i < kNumCfgs && usable(i)) return i;
   }
-  (void)f16x;
-  if (K == 3072) {
-    if (N == 5120) return 8;
-    if (N == 16384) return 7;
-    if (N == 3072) return 8;
-    if (N > 65536) return 19;
+  if (paired) {
+    if (K == 3072 && N == 5120) return 0;
+    if (K == 3072 && N == 16384) return 6;
+  } else {
+    if (K == 3072) {
+      if (N == 5120) return 8;
+      if (N == 16384) return 7;
+      if (N == 3072) return 8;
+      if (N > 65536) return 19;
+    }
+    if (K == 8192 && N == 3072) return 10;
   }
-  if (K == 8192 && N == 3072) return 10;
   const int64_t cpr = K / 32;
-  int best = 22;
+  int best = paired ? -1 : 22;
   double best_score = 1e30;
   for (int i = 0; i < kNumCfgs; ++i) {
     const Cfg& c = kCfgs[i];
-    if (c.multi || !cfg_fits(c, N, K)) continue;
+    if (c.multi || !usable(i)) continue;
     const int64_t span = static_cast<int64_t>(c.lpr) * c.cpl;
     const double k_waste = static_cast<double>(span) / cpr;
     const int64_t blocks = (N + rows_per_block(c) - 1) / rows_per_block(c);
@@ -527,9 +643,12 @@ int set_lds_limit(KernelFn fn, size_t bytes) {
 int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
                    int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg,
                    int grid_override, hipStream_t stream, int prologue = kProNone, const float* aux = nullptr,
-                   float eps = 0.0f) {
+                   float eps = 0.0f, int epilogue = kEpiNone, const EpiArgs& ea = EpiArgs{}) {
   const bool f16x = x_dtype == Q4_F16, f16y = y_dtype == Q4_F16;
-  int ci = cfg >= 0 && cfg < kNumCfgs ? cfg : choose_cfg(N, K, f16x);
+  const bool paired = epilogue != kEpiNone;
+  int ci = cfg >= 0 && cfg < kNumCfgs ? cfg : choose_cfg(N, K, paired);
+  if (paired && (ci < 0 || kCfgs[ci].r != 2 || kCfgs[ci].multi || !cfg_fits(kCfgs[ci], N, K)))
+    return Q4_ERR_UNSUPPORTED;
   if (!cfg_fits(kCfgs[ci], N, K)) ci = 22;
   const Cfg& c = kCfgs[ci];
   const int threads = c.waves * 64;
@@ -540,18 +659,22 @@ int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x
   const bool vec = (K % 32 == 0) && pow2_group && K <= kMaxK && cfg_fits(c, N, K) &&
                    N * (K / 2) < (int64_t{1} << 31) && max_row * (K / 2) < (int64_t{1} << 32) &&
                    aligned(qweight, 16) && aligned(x, 16);
-  if (!vec && prologue != kProNone) return Q4_ERR_UNSUPPORTED;
+  if (!vec && (prologue != kProNone || paired)) return Q4_ERR_UNSUPPORTED;
   if (!vec) {
     const dim3 grid(static_cast<unsigned>((N + 3) / 4)), block(256);
-    if (f16x && f16y) hipLaunchKernelGGL((q4_gemv_generic<true, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
-    else if (f16x) hipLaunchKernelGGL((q4_gemv_generic<true, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
-    else if (f16y) hipLaunchKernelGGL((q4_gemv_generic<false, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
-    else hipLaunchKernelGGL((q4_gemv_generic<false, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f);
+    const EpiArgs none{};
+    if (f16x && f16y) hipLaunchKernelGGL((q4_gemv_generic<true, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f, none);
+    else if (f16x) hipLaunchKernelGGL((q4_gemv_generic<true, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f, none);
+    else if (f16y) hipLaunchKernelGGL((q4_gemv_generic<false, true>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f, none);
+    else hipLaunchKernelGGL((q4_gemv_generic<false, false>), grid, block, 0, stream, qweight, scales, x, y, residual, (int)N, (int)K, group, nullptr, 0.0f, none);
     return launch_status();
   }
   KernelFn fn = f16x ? (f16y ? kTabF16F16[ci] : kTabF16F32[ci]) : (f16y ? kTabF32F16[ci] : kTabF32F32[ci]);
   if (prologue == kProNorm) fn = kTabNorm[ci];
   if (prologue == kProSwiglu) fn = kTabSwiglu[ci];
+  if (epilogue == kEpiSwiglu) fn = prologue == kProNorm ? kTabNormEpiSwiglu[ci] : kTabEpiSwiglu[ci];
+  if (epilogue == kEpiRope) fn = prologue == kProNorm ? kTabNormEpiRope[ci] : kTabEpiRope[ci];
+  if (!fn) return Q4_ERR_UNSUPPORTED;
   const size_t lds = f16x ? lds_bytes<true>(K) : lds_bytes<false>(K);
   if (int st = set_lds_limit(fn, lds)) return st;
   const int64_t blocks = (N + rows_per_block(c) - 1) / rows_per_block(c);
@@ -563,7 +686,7 @@ int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x
     if (grid_override > 0) grid = grid_override < blocks ? grid_override : blocks;
   }
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(threads), lds, stream, qweight, scales, x, y,
-                     residual, (int)N, (int)K, __builtin_ctz(gchunks), aux, eps);
+                     residual, (int)N, (int)K, __builtin_ctz(gchunks), aux, eps, ea);
   return launch_status();
 }
 
@@ -613,4 +736,29 @@ extern "C" int q4_gemv_fused(const int32_t* qweight, const uint16_t* scales, con
   if (static_cast<const void*>(x) == static_cast<const void*>(y)) return Q4_ERR_SHAPE;
   return q4::q4_gemv_launch(qweight, scales, x, Q4_F32, y, Q4_F32, residual, N, K, group, -1, 0,
                             q4::as_stream(stream), prologue, aux, eps);
+}
+
+extern "C" int q4_gemv_epilogue(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
+                                const float* aux, float eps, int epilogue, const q4_rope_kv* rope, float* y,
+                                int64_t N, int64_t K, int group, void* stream) {
+  if (int st = gemv_args(qweight, scales, x, Q4_F32, y, Q4_F32, nullptr, N, K, group)) return st;
+  if (prologue != Q4_PRO_NONE && prologue != Q4_PRO_RMSNORM) return Q4_ERR_DTYPE;
+  if (epilogue != Q4_EPI_SWIGLU && epilogue != Q4_EPI_ROPE_KV) return Q4_ERR_DTYPE;
+  if (prologue == Q4_PRO_RMSNORM && !aux) return Q4_ERR_NULL;
+  if (prologue == Q4_PRO_RMSNORM && !q4::aligned(aux, 16)) return Q4_ERR_ALIGN;
+  if (static_cast<const void*>(x) == static_cast<const void*>(y)) return Q4_ERR_SHAPE;
+  if (N % 2) return Q4_ERR_SHAPE;
+  q4::EpiArgs ea{};
+  if (epilogue == Q4_EPI_ROPE_KV) {
+    if (!rope || !rope->cos_t || !rope->sin_t || !rope->k_cache || !rope->v_cache || !rope->start) return Q4_ERR_NULL;
+    if (rope->n_q <= 0 || rope->n_kv <= 0 || rope->head_dim <= 0 || rope->head_dim % 2 || rope->max_ctx <= 0)
+      return Q4_ERR_SHAPE;
+    if (N != static_cast<int64_t>(rope->n_q + 2 * rope->n_kv) * rope->head_dim) return Q4_ERR_SHAPE;
+    ea = q4::EpiArgs{rope->cos_t, rope->sin_t, rope->k_cache, rope->v_cache, rope->start,
+                     rope->n_q, rope->n_kv, rope->head_dim, rope->max_ctx};
+  }
+  const int pro = prologue == Q4_PRO_RMSNORM ? q4::kProNorm : q4::kProNone;
+  const int epi = epilogue == Q4_EPI_SWIGLU ? q4::kEpiSwiglu : q4::kEpiRope;
+  return q4::q4_gemv_launch(qweight, scales, x, Q4_F32, y, Q4_F32, nullptr, N, K, group, -1, 0,
+                            q4::as_stream(stream), pro, aux, eps, epi, ea);
 }

@@ -11,8 +11,9 @@
 //   o = attention over cache[:L]; h = h + o W_o^T; x = rms_norm(h, ln_post); gu = x W_gu^T;
 //   h = h + (silu(gate) * up) W_down^T
 // then x = rms_norm(h[last], ln_f), logits = x E^T (tied int4 embedding), next = argmax(logits).
-// Projections: C == 1 -> q4_gemv (fp32 in/out, residual fused); C > 1 -> q4_linear (fused int4
-// MFMA GEMM with split-fp16 activations and per-group fp32 scales, residual fused).
+// Projections: C == 1 -> q4_gemv (fp32 in/out, residual fused; norms, RoPE + cache writes and SwiGLU
+// fused into the GEMVs); C > 1 -> q4_linear (fused int4 MFMA GEMM with split-fp16 activations and
+// per-group fp32 scales, residual fused).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -75,11 +76,12 @@ int proj(int C, const float* x, const int32_t* q, const uint16_t* s, float* y, c
   return q4_linear(x, C, q, s, y, res, N, K, group, stream);
 }
 
-// The fused GEMV prologues need the vectorised layout: K % 32 == 0, group = 32 * 2^j, K <= 8192.
-bool gemv_fusable(int D, int inter, int group) {
+// The fused decode GEMVs (qkv and gate/up, K = dim) need the vectorised layout: K % 32 == 0,
+// group = 32 * 2^j, K <= 8192 (the largest paired-row entry covers 256 chunks of 32 per row).
+bool gemv_fusable(int D, int group) {
   const int gc = group / 32;
   const bool pow2 = group % 32 == 0 && gc > 0 && (gc & (gc - 1)) == 0;
-  return pow2 && D % 32 == 0 && inter % 32 == 0 && D <= 8192 && inter <= 8192;
+  return pow2 && D % 32 == 0 && D <= 8192;
 }
 
 }  // namespace
@@ -126,29 +128,31 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
     if (st_ != Q4_OK) return st_; \
   } while (0)
 
-  // Decode (C == 1) uses the GEMVs with fused norm / SwiGLU prologues when the shapes take the
-  // vectorised GEMV (true for every BASELINE model); prefill uses the separate kernels.
-  const bool fused = C == 1 && gemv_fusable(D, m->inter, m->group);
+  // Decode (C == 1), when the shapes take the vectorised GEMV (true for every BASELINE model), runs
+  // five kernels per layer: qkv GEMV with the input norm in its x staging and RoPE + the K/V cache
+  // writes in its epilogue; attention; o-projection + residual; gate/up GEMV with the post-attention
+  // norm and SwiGLU in its epilogue; down-projection + residual. Prefill uses the separate kernels.
+  const bool fused = C == 1 && gemv_fusable(D, m->group);
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
     uint16_t* kc = static_cast<uint16_t*>(caches[2 * i]);
     uint16_t* vc = static_cast<uint16_t*>(caches[2 * i + 1]);
-    if (fused) {  // decode: norms and SwiGLU run inside the GEMVs' x staging
-      Q4_TRY(q4_gemv_fused(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, qkv, nullptr, qkv_w, D,
-                           m->group, stream));
+    if (fused) {
+      const q4_rope_kv rope{m->cos_t, m->sin_t, kc, vc, start, nh, nkv, hd, m->max_ctx};
+      Q4_TRY(q4_gemv_epilogue(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV, &rope, qkv,
+                              qkv_w, D, m->group, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, stream));
+      Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     }
-    Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
     Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, stream));
     if (fused) {
-      Q4_TRY(q4_gemv_fused(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, gu, nullptr, 2 * m->inter, D,
-                           m->group, stream));
-      Q4_TRY(q4_gemv_fused(ly.wdown_q, ly.wdown_s, gu, Q4_PRO_SWIGLU, nullptr, 0.0f, h, h, D, m->inter, m->group,
-                           stream));
+      Q4_TRY(q4_gemv_epilogue(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU, nullptr, act,
+                              2 * m->inter, D, m->group, stream));
+      Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, stream));

@@ -62,6 +62,47 @@ def q4_gemv(qweight, scales, x, group, out_dtype=torch.float32, residual=None, o
     return out
 
 
+class RopeKV(C.Structure):
+    """struct q4_rope_kv of include/q4llm.h."""
+    _fields_ = [("cos_t", C.c_void_p), ("sin_t", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p),
+                ("start", C.c_void_p), ("n_q", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("max_ctx", C.c_int)]
+
+
+PRO_NONE, PRO_RMSNORM = 0, 1
+EPI_SWIGLU, EPI_ROPE_KV = 1, 2
+
+
+def q4_gemv_swiglu(qweight, scales, x, group, norm_w=None, eps=1e-5, out=None):
+    """Decode gate/up GEMV with the SwiGLU epilogue: W = [gate | up] [2I, K] -> silu(W_g x') * (W_u x')
+    [I], x' = rms_norm(x, norm_w, eps) when norm_w is given, else x (llama_q4.py:234-236)."""
+    _dev(qweight, scales, x, norm_w)
+    n, kw = qweight.shape
+    x = x.reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty(n // 2, dtype=torch.float32, device=x.device)
+    pro = PRO_RMSNORM if norm_w is not None else PRO_NONE
+    LIB.call("q4_gemv_epilogue", ptr(qweight), ptr(scales), ptr(x), pro, ptr(norm_w), eps, EPI_SWIGLU, None,
+             ptr(out), n, kw * 8, group, stream_of(x.device))
+    return out
+
+
+def q4_gemv_rope_kv(qweight, scales, x, group, cos_t, sin_t, k_cache, v_cache, start, n_q, n_kv, hd,
+                    norm_w=None, eps=1e-5, out=None):
+    """Decode qkv GEMV with the RoPE + KV-write epilogue: qkv = W x' with q, k rotated at
+    pos = start[0]; k, v rows stored as fp16 at cache row pos (llama_q4.py:215-223)."""
+    _dev(qweight, scales, x, cos_t, sin_t, k_cache, v_cache, start, norm_w)
+    n, kw = qweight.shape
+    x = x.reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=x.device)
+    rope = RopeKV(ptr(cos_t), ptr(sin_t), ptr(k_cache), ptr(v_cache), ptr(start), n_q, n_kv, hd, k_cache.shape[0])
+    pro = PRO_RMSNORM if norm_w is not None else PRO_NONE
+    LIB.call("q4_gemv_epilogue", ptr(qweight), ptr(scales), ptr(x), pro, ptr(norm_w), eps, EPI_ROPE_KV,
+             C.addressof(rope), ptr(out), n, kw * 8, group, stream_of(x.device))
+    return out
+
+
 def q4_gemv_cfg(qweight, scales, x, group, out, cfg=-1, grid=0):
     """Benchmark hook: q4_gemv with an explicit tile config index and grid size."""
     n, kw = qweight.shape

@@ -158,3 +158,63 @@ def test_gemv_fused_swiglu_residual(dev, n, k, group):
     qd, sd_, gud = qw.to(dev), sc.to(dev), gu.to(dev)  # keep the device tensors alive
     LIB.call("q4_gemv_fused", ptr(qd), ptr(sd_), ptr(gud), 2, None, 0.0, ptr(hd), ptr(hd), n, k, group, stream_of(dev))
     assert (hd.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+
+
+@pytest.mark.parametrize("inter,k,group,norm", [(8192, 3072, 128, True), (704, 256, 32, True), (512, 256, 32, False)])
+def test_gemv_epilogue_swiglu(dev, inter, k, group, norm):
+    """q4_gemv_epilogue(SWIGLU): act = silu(W_g x') * (W_u x'), x' = rms_norm(h) (llama_q4.py:234-236)."""
+    g = torch.Generator().manual_seed(inter + k + 3)
+    wq = torch.randn(2 * inter, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(wq, group)
+    h = torch.randn(k, generator=g) * 3
+    lnw = torch.rand(k, generator=g) + 0.5
+    xn = R.rms_norm(h[None], lnw, 1e-5)[0] if norm else h
+    gu = R.dequantize_q4(qw, sc, group).double() @ xn.double()
+    ref = torch.nn.functional.silu(gu[:inter]) * gu[inter:]
+    rms = ref.pow(2).mean().sqrt().item()
+    qd, sd_, hd, lw = qw.to(dev), sc.to(dev), h.to(dev), lnw.to(dev)
+    out = torch.full((inter,), float("nan"), device=dev)
+    ops.q4_gemv_swiglu(qd, sd_, hd, group, norm_w=lw if norm else None, out=out)
+    assert (out.cpu().double() - ref).abs().max().item() <= 2e-5 * rms
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,k,group,pos", [(24, 8, 128, 3072, 128, 700), (4, 2, 64, 256, 32, 0),
+                                                      (4, 2, 64, 256, 32, 127), (4, 2, 64, 256, 32, 128)])
+def test_gemv_epilogue_rope_kv(dev, n_q, n_kv, hd, k, group, pos):
+    """q4_gemv_epilogue(ROPE_KV): qkv = W rms_norm(h); q, k rotated at pos (x cos + rotate_half(x) sin,
+    llama_q4.py:205-207, 218-221); k and v rows written as fp16 at cache row pos (llama_q4.py:222-223).
+    pos == max_ctx: y unrotated, caches untouched."""
+    from q4llm import rope
+    max_ctx = 128 if k == 256 else 1024
+    cfg = synth.TINY if k == 256 else synth.LLAMA32_3B
+    cos_t, sin_t = rope.rope_tables(cfg, max_ctx)
+    n = (n_q + 2 * n_kv) * hd
+    g = torch.Generator().manual_seed(n + k + pos)
+    wq = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(wq, group)
+    h = torch.randn(k, generator=g) * 3
+    lnw = torch.rand(k, generator=g) + 0.5
+    xn = R.rms_norm(h[None], lnw, 1e-5)[0]
+    qkv = (R.dequantize_q4(qw, sc, group).double() @ xn.double()).reshape(n_q + 2 * n_kv, hd)
+    ref = qkv.clone()
+    if pos < max_ctx:
+        c, s = cos_t[pos].double(), sin_t[pos].double()
+        ref[: n_q + n_kv] = qkv[: n_q + n_kv] * c + R.rotate_half(qkv[: n_q + n_kv]) * s
+    rms = ref.pow(2).mean().sqrt().item()
+    kc = torch.full((max_ctx, n_kv, hd), 7.0, dtype=torch.float16, device=dev)
+    vc = torch.full((max_ctx, n_kv, hd), 7.0, dtype=torch.float16, device=dev)
+    start = torch.tensor([pos], dtype=torch.int32, device=dev)
+    qd, sd_, hd_, lw = qw.to(dev), sc.to(dev), h.to(dev), lnw.to(dev)
+    cd, sd2 = cos_t.to(dev), sin_t.to(dev)
+    y = ops.q4_gemv_rope_kv(qd, sd_, hd_, group, cd, sd2, kc, vc, start, n_q, n_kv, hd, norm_w=lw)
+    torch.cuda.synchronize()
+    assert (y.cpu().double().reshape_as(ref) - ref).abs().max().item() <= 1e-5 * rms
+    kcc, vcc = kc.cpu().double(), vc.cpu().double()
+    untouched = torch.ones(max_ctx, dtype=torch.bool)
+    if pos < max_ctx:
+        untouched[pos] = False
+        kref, vref = ref[n_q: n_q + n_kv], ref[n_q + n_kv:]
+        # fp16 rounding of a value within 1e-5 rms of the reference
+        assert ((kcc[pos] - kref).abs() <= 1e-5 * rms + kref.abs() * 2.0 ** -11).all()
+        assert ((vcc[pos] - vref).abs() <= 1e-5 * rms + vref.abs() * 2.0 ** -11).all()
+    assert (kcc[untouched] == 7.0).all() and (vcc[untouched] == 7.0).all()
