@@ -639,12 +639,24 @@ int set_lds_limit(KernelFn fn, size_t bytes) {
 
 }  // namespace
 
+// Matrix-core GEMV for fp32 x / fp32 y (q4_gemv_mx.hip); Q4_ERR_UNSUPPORTED for shapes it does not
+// take. `ep` points at an EpiArgs (same field order as the kernel's own struct).
+int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
+                   const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
+                   const void* ep, hipStream_t stream);
+
 // Runs config `cfg` (-1 = automatic choice) with `grid_override` workgroups (0 = automatic).
+// Automatic fp32-x / fp32-y launches go to the matrix-core kernel when it takes the shape.
 int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
                    int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg,
                    int grid_override, hipStream_t stream, int prologue = kProNone, const float* aux = nullptr,
                    float eps = 0.0f, int epilogue = kEpiNone, const EpiArgs& ea = EpiArgs{}) {
   const bool f16x = x_dtype == Q4_F16, f16y = y_dtype == Q4_F16;
+  if (cfg < 0 && !f16x && !f16y && prologue != kProSwiglu) {
+    const int st = gemv_mx_launch(qweight, scales, static_cast<const float*>(x), aux, eps, static_cast<float*>(y),
+                                  residual, N, K, group, prologue, epilogue, &ea, stream);
+    if (st != Q4_ERR_UNSUPPORTED) return st;
+  }
   const bool paired = epilogue != kEpiNone;
   int ci = cfg >= 0 && cfg < kNumCfgs ? cfg : choose_cfg(N, K, paired);
   if (paired && (ci < 0 || kCfgs[ci].r != 2 || kCfgs[ci].multi || !cfg_fits(kCfgs[ci], N, K)))
