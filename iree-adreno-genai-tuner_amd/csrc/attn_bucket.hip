@@ -16,6 +16,7 @@
 #include "q4_common.h"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace q4 {
 namespace {
@@ -37,6 +38,8 @@ AttnPlan plan_for(int C, int n_q, int n_kv, int L) {
   if (C == 1) {
     p.CB = 1;
     p.S = L <= 1024 ? 32 : (L <= 2048 ? 64 : 128);
+    const char* ov = getenv("Q4_ATTN_S");  // sweep override: keys per split (32, 64 or 128)
+    if (ov && (atoi(ov) == 32 || atoi(ov) == 64 || atoi(ov) == 128)) p.S = atoi(ov);
   } else {
     p.CB = kMaxQ / g < C ? kMaxQ / g : C;
     p.S = 64;
@@ -244,27 +247,33 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 }
 
 // Merge the splits of each (row, head): o = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
-// One workgroup of HD threads per (row, head); splits past the row's position are skipped. The
-// (m, l) pairs are read in parallel (one split per thread, looping when n_splits > HD), the max and
-// the denominator are block reductions, and the o partials are loaded eight splits at a time.
+// One workgroup of HD threads per (row, head); only the splits holding keys <= pos are read. Every
+// load of the first kBatch splits is issued before any use (thread d holds split d's (m, l) and
+// its own dim of kBatch o partials), so the merge costs one memory round trip; the max and the
+// denominator are block reductions through LDS, the numerator is summed in ascending split order.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
                                                          float* __restrict__ out, int n_q, int n_splits, int S,
                                                          const int32_t* __restrict__ start_p) {
+  constexpr int kBatch = 32;
+  constexpr int NW = HD / 64 > 0 ? HD / 64 : 1;
   __shared__ float wts[512];
-  __shared__ float red[HD / 64 > 0 ? HD / 64 : 1];
+  __shared__ float red[NW];
   const int c = blockIdx.x / n_q, h = blockIdx.x % n_q;
   const int d = threadIdx.x;
   const int pos = start_p[0] + c;
   const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos (n_splits <= 512: host)
   const size_t base = (static_cast<size_t>(c) * n_q + h) * n_splits;
+  float ov[kBatch];
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) ov[j] = j < ns ? ws_o[(base + j) * HD + d] : 0.0f;
   float mloc = -INFINITY;
   for (int i = d; i < ns; i += HD) mloc = fmaxf(mloc, ws_ml[2 * (base + i)]);
-  mloc = group_max<64>(mloc);
-  if ((d & 63) == 0) red[d >> 6] = mloc;
+  const float mw = group_max<64>(mloc);
+  if ((d & 63) == 0) red[d >> 6] = mw;
   __syncthreads();
   float M = red[0];
-  for (int w = 1; w < HD / 64; ++w) M = fmaxf(M, red[w]);
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, red[w]);
   __syncthreads();
   float den = 0.0f;
   for (int i = d; i < ns; i += HD) {
@@ -277,17 +286,12 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   if ((d & 63) == 0) red[d >> 6] = den;
   __syncthreads();
   float D = 0.0f;
-  for (int w = 0; w < HD / 64; ++w) D += red[w];
+  for (int w = 0; w < NW; ++w) D += red[w];
   float num = 0.0f;
-  int i = 0;
-  for (; i + 8 <= ns; i += 8) {
-    float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = ws_o[(base + i + j) * HD + d];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) num = fmaf(wts[i + j], v[j], num);
-  }
-  for (; i < ns; ++i) num = fmaf(wts[i], ws_o[(base + i) * HD + d], num);
+  for (int j = 0; j < kBatch; ++j)
+    if (j < ns) num = fmaf(wts[j], ov[j], num);
+  for (int i = kBatch; i < ns; ++i) num = fmaf(wts[i], ws_o[(base + i) * HD + d], num);
   out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / D;
 }
 
