@@ -6,15 +6,20 @@
 // explicit list of CDNA4 tiles and a fixed rule picks one per shape.
 //
 // Kernel structure:
-//   * block tile BM x BN, K step BK = 64; WGM x WGN waves, each owning a (BM/WGM) x (BN/WGN) tile
-//     made of 32x32 v_mfma_f32_32x32x16_f16 tiles;
-//   * A and B tiles are staged global -> registers -> LDS, double buffered: the loads of step k+1
-//     are in flight while step k runs on the matrix cores;
-//   * LDS rows are padded by 16 bytes so the 16-byte operand reads of a wave are conflict free;
-//   * global reads are raw buffer loads: rows past M/N and k past K read out of range and return
+//   * block tile BM x BN, K step BK = 64 or 32 (one 128- or 64-byte LDS row per operand row);
+//     WM x WN waves, each owning a (BM/WM) x (BN/WN) tile of 32x32 v_mfma_f32_32x32x16_f16 tiles;
+//   * NST-stage ring of LDS stages filled by direct global -> LDS 16-byte loads (buffer loads with
+//     the LDS bit, gfx950): no VGPRs are spent on staging, and the loads of the next NST-1 K steps
+//     are in flight while the current step runs on the matrix cores; each wave waits only for the
+//     oldest stage's loads (an exact vmcnt), then one barrier per K step publishes the stage and
+//     frees the one read in the previous step;
+//   * a direct load writes 64 lanes x 16 bytes contiguously (1 KB of whole rows), so the layout is
+//     chosen on the global side: the lane for LDS slot s of row r fetches chunk s ^ swz(r), which
+//     makes the MFMA operand reads conflict free without padding (see swz below);
+//   * global reads are raw buffer loads: rows past M/N and k past K read out of range and land as
 //     zeros, so ragged edges need no branches;
-//   * workgroups are ordered XCD-major: consecutive tiles along N land on the same XCD and share
-//     its L2 for the A panel.
+//   * workgroups are ordered XCD-major and grouped: each XCD gets a compact block of tiles (4 tile
+//     rows at a time), so its A and B panel slices are reused from its own L2.
 // MFMA operand layout used: lane l supplies row (l % 32) of A (column of B) and 8 consecutive k at
 // 8 * (l / 32); A and B use the same k pattern, so the product is independent of the order in which
 // the hardware consumes the k elements of a lane. Accumulator j of lane l holds
@@ -30,8 +35,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 64;
-constexpr int PITCH = BK + 8;  // LDS row pitch in halfs (16-byte pad)
+constexpr uint32_t kOOB = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
@@ -42,78 +46,110 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int BM, int BN, int WGM, int WGN>
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes land at dst + 16 i (dst
+// is wave-uniform). Out-of-range offsets land zeros.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 16, off,
+                                           0, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int WM, int WN, int NST, int BK>
 struct GemmCfg {
-  static constexpr int kWaves = WGM * WGN;
+  static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int WTM = BM / WGM;  // wave tile
-  static constexpr int WTN = BN / WGN;
-  static constexpr int TM = WTM / 32;   // 32x32 MFMA tiles per wave
+  static constexpr int WTM = BM / WM;  // wave tile
+  static constexpr int WTN = BN / WN;
+  static constexpr int TM = WTM / 32;  // 32x32 MFMA tiles per wave
   static constexpr int TN = WTN / 32;
-  static constexpr int A_CH = BM * BK / 8;  // 16-byte chunks per A tile
-  static constexpr int B_CH = BN * BK / 8;
-  static constexpr int A_LD = (A_CH + kThreads - 1) / kThreads;
-  static constexpr int B_LD = (B_CH + kThreads - 1) / kThreads;
-  static constexpr size_t kLds = 2ull * (BM + BN) * PITCH * 2;
+  static constexpr int kRow = BK * 2;                  // bytes per LDS row: 128 (BK 64) or 64 (BK 32)
+  static constexpr int kRowsPerInst = 1024 / kRow;     // rows one direct-load instruction fills
+  static constexpr int kStage = (BM + BN) * kRow;
+  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage;
+  static constexpr int kAI = BM / kRowsPerInst / kWaves;  // direct-load instructions per wave and stage
+  static constexpr int kBI = BN / kRowsPerInst / kWaves;
+  static constexpr int kLPW = kAI + kBI;
+  static_assert(BK == 32 || BK == 64, "K step");
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 MFMA tile");
+  static_assert(kAI * kRowsPerInst * kWaves == BM && kBI * kRowsPerInst * kWaves == BN,
+                "row blocks of the direct loads must divide over the waves");
+  static_assert(NST >= 2 && NST <= 4 && kLPW * (NST - 2) < 64, "stage count");
 };
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f16_nt_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ Cm, int M, int N, int K,
-    int lda, int ldb, int ldc, int tiles_m, int tiles_n, int k_per_split, int xcd_remap) {
-  using G = GemmCfg<BM, BN, WGM, WGN>;
-  extern __shared__ uint4 smem4[];
-  uint16_t* lds = reinterpret_cast<uint16_t*>(smem4);
-  uint16_t* As[2] = {lds, lds + BM * PITCH};
-  uint16_t* Bs[2] = {lds + 2 * BM * PITCH, lds + 2 * BM * PITCH + BN * PITCH};
+// LDS swizzle: chunk c (16 bytes) of tile row r sits at slot c ^ swz(r). The LDS serves 16 lanes x
+// 16 bytes per clock from 16 bank groups (256 bytes); an MFMA operand read takes 16 consecutive
+// rows at one chunk, which the swizzle spreads over all 16 groups:
+//   BK 64 (128-byte rows, 2 per 256 bytes): swz(r) = (r >> 1) & 7;
+//   BK 32 (64-byte rows, 4 per 256 bytes):  swz(r) = (r >> 2) & 3.
+template <int BK>
+__device__ __forceinline__ int swz(int r) {
+  return BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3;
+}
 
-  // XCD-major tile order: workgroup b runs on XCD b % 8; give XCD x a contiguous tile range.
+template <int BM, int BN, int WM, int WN, int NST, int BK>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ Cm, int M, int N, int K,
+    int lda, int ldb, int ldc, int tiles_m, int tiles_n, int xcd_remap) {
+  using G = GemmCfg<BM, BN, WM, WN, NST, BK>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+
+  // XCD-major tile order: workgroup b runs on XCD b % 8; give XCD x a contiguous range of the
+  // tile sequence. The sequence walks groups of kGroupM tile rows column by column, so the range an
+  // XCD holds is a compact block (4 x 8 tiles for 32 tiles) whose A and B panels stay in its L2.
   int bid = blockIdx.x;
   const int ntiles = tiles_m * tiles_n;
   if (xcd_remap) bid = (bid % 8) * (ntiles / 8) + bid / 8;
-  const int tm = bid / tiles_n, tn = bid % tiles_n;
+  constexpr int kGroupM = 4;
+  const int group = bid / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int in_group = bid - group * (kGroupM * tiles_n);
+  const int tm = first_m + in_group % gsize, tn = in_group / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kz = blockIdx.y;  // split-K slice
-  const int kbeg = kz * k_per_split;
-  const int kend = min(K, kbeg + k_per_split);
 
   const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, static_cast<uint32_t>(M - 1) * lda * 2u + K * 2u);
   const __amdgpu_buffer_rsrc_t br = make_rsrc(B, static_cast<uint32_t>(N - 1) * ldb * 2u + K * 2u);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WGN, wn = wave % WGN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
 
-  uint4 ra[G::A_LD], rb[G::B_LD];
-  auto gload = [&](int k0) {
+  // Direct loads: instruction j of this wave fills row block b = wave + j * kWaves (kRowsPerInst
+  // rows) of the stage; the lane for LDS slot s = lane % (BK / 8) of tile row
+  // r = b * kRowsPerInst + lane / (BK / 8) fetches chunk s ^ swz(r).
+  constexpr int kCpr = BK / 8;  // chunks per row
+  uint32_t aoff[G::kAI], boff[G::kBI];
+  int achunk[G::kAI], bchunk[G::kBI];
 #pragma unroll
-    for (int i = 0; i < G::A_LD; ++i) {
-      const int ch = tid + i * G::kThreads;
-      const int r = ch / (BK / 8), c8 = ch % (BK / 8);
-      const int row = m0 + r, k = k0 + c8 * 8;
-      const bool ok = ch < G::A_CH && row < M && k < kend;
-      ra[i] = buf_load16(ar, ok ? (static_cast<uint32_t>(row) * lda + k) * 2u : 0x80000000u);
-    }
+  for (int j = 0; j < G::kAI; ++j) {
+    const int r = (wave + j * G::kWaves) * G::kRowsPerInst + lane / kCpr;
+    achunk[j] = (lane % kCpr) ^ swz<BK>(r);
+    aoff[j] = m0 + r < M ? static_cast<uint32_t>(m0 + r) * lda * 2u + achunk[j] * 16u : kOOB;
+  }
 #pragma unroll
-    for (int i = 0; i < G::B_LD; ++i) {
-      const int ch = tid + i * G::kThreads;
-      const int r = ch / (BK / 8), c8 = ch % (BK / 8);
-      const int row = n0 + r, k = k0 + c8 * 8;
-      const bool ok = ch < G::B_CH && row < N && k < kend;
-      rb[i] = buf_load16(br, ok ? (static_cast<uint32_t>(row) * ldb + k) * 2u : 0x80000000u);
-    }
-  };
-  auto lstore = [&](int s) {
+  for (int j = 0; j < G::kBI; ++j) {
+    const int r = (wave + j * G::kWaves) * G::kRowsPerInst + lane / kCpr;
+    bchunk[j] = (lane % kCpr) ^ swz<BK>(r);
+    boff[j] = n0 + r < N ? static_cast<uint32_t>(n0 + r) * ldb * 2u + bchunk[j] * 16u : kOOB;
+  }
+  auto issue = [&](int kt, int stage) {
+    const int k0 = kt * BK;
+    unsigned char* sa = lds + stage * G::kStage;
+    unsigned char* sb = sa + BM * G::kRow;
 #pragma unroll
-    for (int i = 0; i < G::A_LD; ++i) {
-      const int ch = tid + i * G::kThreads;
-      if (ch < G::A_CH) *reinterpret_cast<uint4*>(As[s] + (ch / (BK / 8)) * PITCH + (ch % (BK / 8)) * 8) = ra[i];
-    }
+    for (int j = 0; j < G::kAI; ++j)
+      load_lds16(ar, sa + (wave + j * G::kWaves) * 1024,
+                 k0 + 8 * achunk[j] < K && aoff[j] != kOOB ? aoff[j] + k0 * 2u : kOOB);
 #pragma unroll
-    for (int i = 0; i < G::B_LD; ++i) {
-      const int ch = tid + i * G::kThreads;
-      if (ch < G::B_CH) *reinterpret_cast<uint4*>(Bs[s] + (ch / (BK / 8)) * PITCH + (ch % (BK / 8)) * 8) = rb[i];
-    }
+    for (int j = 0; j < G::kBI; ++j)
+      load_lds16(br, sb + (wave + j * G::kWaves) * 1024,
+                 k0 + 8 * bchunk[j] < K && boff[j] != kOOB ? boff[j] + k0 * 2u : kOOB);
   };
 
   float16v acc[G::TM][G::TN];
@@ -124,37 +160,47 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f16_nt_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int nk = (kend - kbeg + BK - 1) / BK;
-  gload(kbeg);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < nk) gload(kbeg + (kt + 1) * BK);
+  // Operand reads: row r of the tile at chunk c lives at r * kRow + ((c ^ swz(r)) << 4); the rows
+  // read start at multiples of 32, so swz(r) == swz(lane & 31).
+  const int arow = wm * G::WTM + (lane & 31);
+  const int brow = wn * G::WTN + (lane & 31);
+  auto compute = [&](int stage) {
+    const unsigned char* sa = lds + stage * G::kStage;
+    const unsigned char* sb = sa + BM * G::kRow;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int sw = ((2 * kk + (lane >> 5)) ^ swz<BK>(lane & 31)) << 4;
       half8 af[G::TM], bf[G::TN];
 #pragma unroll
-      for (int i = 0; i < G::TM; ++i) {
-        const int r = wm * G::WTM + i * 32 + (lane & 31);
-        af[i] = *reinterpret_cast<const half8*>(As[s] + r * PITCH + kk + 8 * (lane >> 5));
-      }
+      for (int i = 0; i < G::TM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + (arow + 32 * i) * G::kRow + sw);
 #pragma unroll
-      for (int j = 0; j < G::TN; ++j) {
-        const int r = wn * G::WTN + j * 32 + (lane & 31);
-        bf[j] = *reinterpret_cast<const half8*>(Bs[s] + r * PITCH + kk + 8 * (lane >> 5));
-      }
+      for (int j = 0; j < G::TN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + (brow + 32 * j) * G::kRow + sw);
 #pragma unroll
       for (int i = 0; i < G::TM; ++i)
 #pragma unroll
         for (int j = 0; j < G::TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) lstore(s ^ 1);
-    __syncthreads();
+  };
+
+  const int nk = (K + BK - 1) / BK;
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nk) issue(s, s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // This wave's loads of stage kt are complete once at most `after` later stages are in flight.
+    const int after = min(NST - 2, nk - 1 - kt);
+    if (after >= 2) wait_vmcnt<(NST >= 4 ? 2 * G::kLPW : 0)>();
+    else if (after == 1) wait_vmcnt<(NST >= 3 ? G::kLPW : 0)>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's stage-kt loads landed; stage kt-1 is no longer read
+    asm volatile("" ::: "memory");
+    if (kt + NST - 1 < nk) issue(kt + NST - 1, (kt + NST - 1) % NST);
+    compute(kt % NST);
   }
 
-  // Epilogue: fp16 stores (split-K slices > 0 never occur on this path; see host).
+  // Epilogue: fp16 stores (lane l holds column l % 32 of each 32x32 tile).
 #pragma unroll
   for (int i = 0; i < G::TM; ++i)
 #pragma unroll
@@ -191,44 +237,57 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
 }
 
 struct TileCfg {
-  int bm, bn, wgm, wgn;
+  int bm, bn, wgm, wgn, nst, bk;
 };
-// Explicit CDNA4 tile list (index stable for q4_gemm_cfg / Q4_GEMM_CFG).
+// Explicit CDNA4 tile list (index stable for gemm_f16_nt_cfg / Q4_GEMM_CFG).
 constexpr TileCfg kTiles[] = {
-    {256, 256, 2, 2},  // 0: large square problems (1 workgroup per CU at 4096^2)
-    {256, 128, 2, 2},  // 1
-    {128, 128, 2, 2},  // 2
-    {128, 64, 2, 2},   // 3: M = 256 prefill shapes: enough workgroups for 256 CUs
-    {64, 64, 2, 2},    // 4: small / skinny problems
+    {256, 256, 2, 4, 2, 64},  // 0: 8 waves of 128x64, 2 stages of K 64 (128 KB LDS)
+    {256, 128, 4, 2, 3, 64},  // 1: 8 waves of 64x64, 3 stages (144 KB)
+    {128, 256, 2, 4, 3, 64},  // 2: 8 waves of 64x64, 3 stages (144 KB)
+    {128, 128, 2, 2, 4, 64},  // 3: 4 waves of 64x64, 4 stages (128 KB)
+    {128, 128, 2, 2, 2, 64},  // 4: 4 waves of 64x64, 2 stages (64 KB, two workgroups per CU)
+    {128, 64, 2, 2, 4, 64},   // 5: 4 waves of 64x32, 4 stages (96 KB)
+    {64, 64, 2, 2, 4, 64},    // 6: 4 waves of 32x32, 4 stages (64 KB)
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-using GemmFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int, int, int, int, int);
+using GemmFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int, int, int, int);
 
 template <int I>
 constexpr GemmFn gemm_fn() {
-  return gemm_f16_nt_kernel<kTiles[I].bm, kTiles[I].bn, kTiles[I].wgm, kTiles[I].wgn>;
+  constexpr TileCfg t = kTiles[I];
+  return gemm_f16_nt_kernel<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>;
 }
 template <int I>
 constexpr size_t gemm_lds() {
-  return GemmCfg<kTiles[I].bm, kTiles[I].bn, kTiles[I].wgm, kTiles[I].wgn>::kLds;
+  constexpr TileCfg t = kTiles[I];
+  return GemmCfg<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>::kLds;
 }
-constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>()};
-constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(), gemm_lds<4>()};
+constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(),
+                               gemm_fn<4>(), gemm_fn<5>(), gemm_fn<6>()};
+constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(),
+                               gemm_lds<4>(), gemm_lds<5>(), gemm_lds<6>()};
+static_assert(sizeof(kGemmFns) / sizeof(kGemmFns[0]) == kNumTiles, "one kernel per tile entry");
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Fixed rule: the largest tile that still gives at least one full wave of workgroups per CU
-// (256); otherwise the tile with the most workgroups.
+// Fixed rule, from a sweep of every entry over the config-3 shapes on one MI355X: square-ish
+// problems take 256x256 when that alone fills the 256 CUs (4096^3: 1.05 PFLOP/s), else 128x128
+// with two workgroups per CU (2048x3072x8192: 860 TFLOP/s); skinny prefill problems (M < 512) take
+// the largest 4-stage tile that still gives >= 160 workgroups, the deep prefetch hiding the latency
+// of the streamed weights (256x16384x3072: 640 TFLOP/s). The K-32 stage variant (4 stages for
+// 256x256) measured no faster than 2 stages of K 64, so the list keeps K 64 only.
 int choose_tile(int64_t M, int64_t N) {
   const char* ov = getenv("Q4_GEMM_CFG");
   if (ov && *ov) {
     const int i = atoi(ov);
     if (i >= 0 && i < kNumTiles) return i;
   }
-  for (int i = 0; i < kNumTiles; ++i)
-    if (cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn) >= 256) return i;
-  return kNumTiles - 1;
+  auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
+  if (M >= 512) return tiles(0) >= 256 ? 0 : 4;
+  for (int i : {3, 5, 6})
+    if (tiles(i) >= 160) return i;
+  return 6;
 }
 
 }  // namespace
@@ -251,7 +310,7 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
   }
   const int remap = (ntiles % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL(kGemmFns[ti], dim3(ntiles, 1), dim3(64 * t.wgm * t.wgn), lds, st, A, B, C, (int)M, (int)N,
-                     (int)K, (int)lda, (int)ldb, (int)ldc, tiles_m, tiles_n, (int)K, remap);
+                     (int)K, (int)lda, (int)ldb, (int)ldc, tiles_m, tiles_n, remap);
   return launch_status();
 }
 
