@@ -213,27 +213,46 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
       }
 }
 
-// fp16 GEMV for M == 1 (the gemv_nt shape): one wave per 4 rows of B, 16 lanes per row,
-// v_dot2_f32_f16 with fp32 accumulation. Memory bound.
+// fp16 GEMV for M == 1 (the gemv_nt shape): each wave owns kRows rows; its 64 lanes cover K in
+// 16-byte chunks (8 k), kKc chunks per lane per pass, so one pass spans 512 * kKc k. Every load of a
+// pass (x and the rows) is issued before any use; v_dot2_f32_f16 with fp32 accumulation, then a
+// reduction over the wave. Rows past N and k past K read out of range (zeros). Memory bound.
+template <int kRows, int kKc>
 __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ B,
                                                        uint16_t* __restrict__ c, int N, int K, int ldb) {
   typedef _Float16 half2v __attribute__((ext_vector_type(2)));
   const int lane = threadIdx.x & 63;
-  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + lane / 16;
-  const int lr = lane % 16;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
   const __amdgpu_buffer_rsrc_t br = make_rsrc(B, static_cast<uint32_t>(N - 1) * ldb * 2u + K * 2u);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a, K * 2u);
-  float acc = 0.0f;
-  for (int k = lr * 8; k < K; k += 128) {
-    const uint4 w = buf_load16(br, row < N ? (static_cast<uint32_t>(row) * ldb + k) * 2u : 0x80000000u);
-    const uint4 x = buf_load16(xr, k * 2u);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.x), __builtin_bit_cast(half2v, x.x), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.y), __builtin_bit_cast(half2v, x.y), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.z), __builtin_bit_cast(half2v, x.z), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.w), __builtin_bit_cast(half2v, x.w), acc, false);
+  float acc[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
+  for (int kb = 0; kb < K; kb += 512 * kKc) {
+    uint4 xv[kKc], wv[kRows][kKc];
+#pragma unroll
+    for (int i = 0; i < kKc; ++i) {
+      const int k = kb + (i * 64 + lane) * 8;
+      xv[i] = buf_load16(xr, k < K ? k * 2u : kOOB);
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+        wv[r][i] = buf_load16(br, k < K && row0 + r < N ? (static_cast<uint32_t>(row0 + r) * ldb + k) * 2u : kOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < kKc; ++i)
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].x), __builtin_bit_cast(half2v, xv[i].x), acc[r], false);
+        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].y), __builtin_bit_cast(half2v, xv[i].y), acc[r], false);
+        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].z), __builtin_bit_cast(half2v, xv[i].z), acc[r], false);
+        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].w), __builtin_bit_cast(half2v, xv[i].w), acc[r], false);
+      }
   }
-  acc = segment_sum_to_last<16>(acc);
-  if (lr == 15 && row < N) c[row] = float_to_half_bits(acc);
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const float v = group_sum<64>(acc[r]);
+    if (lane == 0 && row0 + r < N) c[row0 + r] = float_to_half_bits(v);
+  }
 }
 
 struct TileCfg {
@@ -294,9 +313,16 @@ int choose_tile(int64_t M, int64_t N) {
 
 int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                     int64_t ldb, int64_t ldc, int cfg, hipStream_t st) {
-  if (M == 1 && cfg < 0) {
-    const unsigned grid = static_cast<unsigned>(cdiv(N, 16));
-    hipLaunchKernelGGL(gemv_f16_kernel, dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
+  if (M == 1 && cfg < 0) {  // 2 rows per wave, 8 per workgroup; passes of up to 4096 k
+    const unsigned grid = static_cast<unsigned>(cdiv(N, 8));
+    if (K <= 1024)
+      hipLaunchKernelGGL((gemv_f16_kernel<2, 2>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
+    else if (K <= 2048)
+      hipLaunchKernelGGL((gemv_f16_kernel<2, 4>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
+    else if (K <= 3072)
+      hipLaunchKernelGGL((gemv_f16_kernel<2, 6>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
+    else
+      hipLaunchKernelGGL((gemv_f16_kernel<2, 8>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
     return launch_status();
   }
   const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N);
