@@ -1,0 +1,491 @@
+// llm-runner: the native generation runner over libq4llm (the MI355X counterpart of the
+// reference's runner/llm_runner.c, which drives IREE-compiled LlamaQ4 modules on Adreno).
+//
+//   llm-runner --weights=model.q4w --prompt=ids.txt [--max_new_tokens=32] [--chunk=128]
+//              [--buckets=256,512,1024,2048,4096] [--schedule=bucketed|max] [--n_layers=N]
+//              [--n_kv_heads=N] [--head_dim=N] [--max_ctx=N] [--stop_ids=a,b] [--warmup=1] [--plan]
+//
+// Kept from llm_runner.c (same flag names and meaning, same schedule, same JSON keys):
+//   * prefill in chunks of --chunk tokens, the last chunk zero-padded, last = n - 1 of the chunk;
+//     bucket = smallest compiled bucket >= start + chunk (llm_runner.c:143-149, 210-222);
+//   * the first generated token comes from prefill; decode at pos = n_prompt, ... with the bucket
+//     >= pos + 1 until --max_new_tokens exist or a stop id appears (:226-245);
+//   * --schedule=max always uses the largest bucket (:18-19, 143-144);
+//   * the runner owns the zeroed KV caches for the whole run and the steps write them in place
+//     (:301-315);
+//   * warm-up: every entry point the schedule will use runs --warmup times before timing (:175-203);
+//   * errors (empty prompt, prompt + new > max_ctx, no bucket) print to stderr and exit 1 (:327-331);
+//   * one JSON object on stdout (:249-262).
+// In place of the IREE module + parameter archive, the weights come from a packed-weight file
+// (q4llm/packed.py) copied once to HBM, and each entry point prefill_c{C}_l{L} / decode_l{L} is one
+// q4llm_step captured into a HIP graph on first use and replayed; per call the host copies the
+// token ids, start and last into pinned buffers, launches the graph and reads back 4 bytes.
+// --plan prints the schedule (the buckets of every prefill chunk and decode step) and exits
+// without touching the GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "q4llm.h"
+
+namespace {
+
+struct Flags {
+  std::string weights, prompt, buckets = "256,512,1024,2048,4096", schedule = "bucketed", stop_ids;
+  int max_new_tokens = 32, chunk = 128, n_layers = -1, n_kv_heads = -1, head_dim = -1, max_ctx = -1, warmup = 1;
+  bool plan = false;
+};
+
+[[noreturn]] __attribute__((format(printf, 1, 2))) void die(const char* fmt, ...) {
+  std::fprintf(stderr, "llm-runner: ");
+  va_list ap;
+  va_start(ap, fmt);
+  std::vfprintf(stderr, fmt, ap);
+  va_end(ap);
+  std::fprintf(stderr, "\n");
+  std::exit(1);
+}
+
+#define HIP_OK(expr)                                                                               \
+  do {                                                                                             \
+    hipError_t e_ = (expr);                                                                        \
+    if (e_ != hipSuccess) {                                                                        \
+      std::fprintf(stderr, "llm-runner: %s failed: %s\n", #expr, hipGetErrorString(e_));           \
+      std::exit(1);                                                                                \
+    }                                                                                              \
+  } while (0)
+
+#define Q4_OK_OR_DIE(expr)                                                                         \
+  do {                                                                                             \
+    int st_ = (expr);                                                                              \
+    if (st_ != Q4_OK) {                                                                            \
+      std::fprintf(stderr, "llm-runner: %s -> %s (hipError %d)\n", #expr, q4llm_status_string(st_), \
+                   q4llm_last_hip_error());                                                        \
+      std::exit(1);                                                                                \
+    }                                                                                              \
+  } while (0)
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// Whitespace/comma separated integers, as parse_ints in llm_runner.c:55-65 (non-numbers skipped).
+std::vector<int32_t> parse_ints(const std::string& s) {
+  std::vector<int32_t> out;
+  const char* p = s.c_str();
+  while (*p) {
+    char* end = nullptr;
+    const long v = std::strtol(p, &end, 10);
+    if (end == p) {
+      ++p;
+      continue;
+    }
+    out.push_back(static_cast<int32_t>(v));
+    p = end;
+  }
+  return out;
+}
+
+Flags parse_flags(int argc, char** argv) {
+  Flags f;
+  for (int i = 1; i < argc; ++i) {
+    std::string a = argv[i];
+    if (a.rfind("--", 0) != 0) die("unexpected argument %s", argv[i]);
+    a = a.substr(2);
+    std::string key = a, val;
+    const size_t eq = a.find('=');
+    if (eq != std::string::npos) {
+      key = a.substr(0, eq);
+      val = a.substr(eq + 1);
+    } else if (key != "plan") {
+      if (i + 1 >= argc) die("flag --%s needs a value", key.c_str());
+      val = argv[++i];
+    }
+    auto num = [&](int* dst) { *dst = std::atoi(val.c_str()); };
+    if (key == "weights") f.weights = val;
+    else if (key == "prompt") f.prompt = val;
+    else if (key == "buckets") f.buckets = val;
+    else if (key == "schedule") f.schedule = val;
+    else if (key == "stop_ids") f.stop_ids = val;
+    else if (key == "max_new_tokens") num(&f.max_new_tokens);
+    else if (key == "chunk") num(&f.chunk);
+    else if (key == "n_layers") num(&f.n_layers);
+    else if (key == "n_kv_heads") num(&f.n_kv_heads);
+    else if (key == "head_dim") num(&f.head_dim);
+    else if (key == "max_ctx") num(&f.max_ctx);
+    else if (key == "warmup") num(&f.warmup);
+    else if (key == "plan") f.plan = val.empty() || val == "1" || val == "true";
+    else die("unknown flag --%s", key.c_str());
+  }
+  if (f.schedule != "bucketed" && f.schedule != "max") die("--schedule must be bucketed or max, not %s", f.schedule.c_str());
+  if (f.chunk <= 0) die("--chunk must be positive");
+  return f;
+}
+
+// Smallest bucket >= needed, the largest under schedule max, -1 if none (llm_runner.c:143-149).
+int pick_bucket(const std::vector<int32_t>& buckets, int needed, bool use_max) {
+  if (use_max) return buckets.back();
+  for (int b : buckets)
+    if (b >= needed) return b;
+  return -1;
+}
+
+struct Plan {
+  std::vector<int> prefill, decode;  // bucket of every prefill chunk and of every possible decode step
+};
+
+Plan make_plan(int n_prompt, int max_new, int C, const std::vector<int32_t>& buckets, int max_ctx, bool use_max) {
+  if (n_prompt == 0) die("empty prompt");
+  const int total = n_prompt + max_new;
+  if (total > max_ctx || ((n_prompt + C - 1) / C) * C > max_ctx)
+    die("prompt %d + new %d exceeds max_ctx %d", n_prompt, max_new, max_ctx);
+  Plan p;
+  for (int start = 0; start < n_prompt; start += C) {
+    const int L = pick_bucket(buckets, start + C, use_max);
+    if (L < 0) die("no bucket >= %d", start + C);
+    p.prefill.push_back(L);
+  }
+  for (int pos = n_prompt; pos < total - 1; ++pos) p.decode.push_back(pick_bucket(buckets, pos + 1, use_max));
+  return p;
+}
+
+std::string read_file(const std::string& path) {
+  FILE* fp = std::fopen(path.c_str(), "rb");
+  if (!fp) die("cannot open --prompt=%s", path.c_str());
+  std::string s;
+  char buf[65536];
+  size_t n;
+  while ((n = std::fread(buf, 1, sizeof buf, fp)) > 0) s.append(buf, n);
+  std::fclose(fp);
+  return s;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Packed-weight file (layout in q4llm/packed.py): ASCII header, then 256-byte aligned tensors.
+// ------------------------------------------------------------------------------------------------
+
+struct TensorMeta {
+  std::string dtype;
+  uint64_t offset = 0, nbytes = 0;
+  std::vector<int64_t> shape;
+};
+
+struct Packed {
+  std::map<std::string, long> ints;
+  float eps = 0.0f;
+  std::map<std::string, TensorMeta> tensors;
+  std::vector<void*> device_buffers;
+  std::map<std::string, void*> dev;
+};
+
+void load_packed(const std::string& path, Packed* pk) {
+  FILE* fp = std::fopen(path.c_str(), "rb");
+  if (!fp) die("cannot open --weights=%s", path.c_str());
+  std::string head(1 << 20, '\0');
+  head.resize(std::fread(&head[0], 1, head.size(), fp));
+  const size_t end = head.find("\nend\n");
+  if (head.rfind("Q4LLM-PACKED 1\n", 0) != 0 || end == std::string::npos) die("%s is not a packed-weight file", path.c_str());
+  size_t pos = head.find('\n') + 1;
+  while (pos <= end) {
+    const size_t nl = head.find('\n', pos);
+    const std::string line = head.substr(pos, nl - pos);
+    pos = nl + 1;
+    char kind[16] = {0}, name[256] = {0}, dt[8] = {0}, val[64] = {0};
+    if (std::sscanf(line.c_str(), "%15s", kind) != 1) continue;
+    if (!std::strcmp(kind, "config")) {
+      if (std::sscanf(line.c_str(), "%*s %255s %63s", name, val) != 2) die("bad header line: %s", line.c_str());
+      if (!std::strcmp(name, "eps")) pk->eps = std::strtof(val, nullptr);
+      else pk->ints[name] = std::strtol(val, nullptr, 10);
+    } else if (!std::strcmp(kind, "tensor")) {
+      unsigned long long off = 0, nb = 0;
+      int nd = 0, used = 0;
+      if (std::sscanf(line.c_str(), "%*s %255s %7s %llu %llu %d%n", name, dt, &off, &nb, &nd, &used) != 5)
+        die("bad tensor line: %s", line.c_str());
+      TensorMeta m;
+      m.dtype = dt;
+      m.offset = off;
+      m.nbytes = nb;
+      const char* q = line.c_str() + used;
+      for (int d = 0; d < nd; ++d) {
+        char* e = nullptr;
+        m.shape.push_back(std::strtoll(q, &e, 10));
+        q = e;
+      }
+      pk->tensors[name] = m;
+    } else if (!std::strcmp(kind, "end")) {
+      break;
+    } else {
+      die("bad header line: %s", line.c_str());
+    }
+  }
+  for (const char* k : {"dim", "n_layers", "n_heads", "n_kv", "head_dim", "inter", "vocab", "group", "max_ctx"})
+    if (!pk->ints.count(k)) die("%s: header lacks config %s", path.c_str(), k);
+  std::vector<char> host;
+  for (auto& kv : pk->tensors) {
+    const TensorMeta& m = kv.second;
+    host.resize(m.nbytes);
+    if (std::fseek(fp, static_cast<long>(m.offset), SEEK_SET) != 0 || std::fread(host.data(), 1, m.nbytes, fp) != m.nbytes)
+      die("%s: tensor %s runs past the end of the file", path.c_str(), kv.first.c_str());
+    void* d = nullptr;
+    HIP_OK(hipMalloc(&d, m.nbytes));
+    HIP_OK(hipMemcpy(d, host.data(), m.nbytes, hipMemcpyHostToDevice));
+    pk->device_buffers.push_back(d);
+    pk->dev[kv.first] = d;
+  }
+  std::fclose(fp);
+}
+
+void* need(Packed& pk, const std::string& name) {
+  auto it = pk.dev.find(name);
+  if (it == pk.dev.end()) die("weights file lacks tensor %s", name.c_str());
+  return it->second;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Entry points: one graph-captured q4llm_step per (C, L)
+// ------------------------------------------------------------------------------------------------
+
+struct EntryPoint {
+  int C = 0, L = 0;
+  int32_t *tokens = nullptr, *start = nullptr, *last = nullptr, *next = nullptr;  // device
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipGraphExec_t exec = nullptr;
+};
+
+struct Runner {
+  q4llm_model model{};
+  std::vector<q4llm_layer> layers;
+  std::vector<void*> caches;
+  hipStream_t stream = nullptr;
+  int32_t* host = nullptr;  // pinned: [0, C) tokens, then start, last, next
+  int host_cap = 0;
+  std::map<std::pair<int, int>, EntryPoint> eps;
+
+  void raw_step(EntryPoint& e) {
+    Q4_OK_OR_DIE(q4llm_step(&model, e.tokens, e.C, e.start, e.last, caches.data(), e.L, e.next, nullptr, e.ws,
+                            e.ws_bytes, stream));
+  }
+
+  EntryPoint& entry(int C, int L) {
+    auto key = std::make_pair(C, L);
+    auto it = eps.find(key);
+    if (it != eps.end()) return it->second;
+    EntryPoint e;
+    e.C = C;
+    e.L = L;
+    HIP_OK(hipMalloc(&e.tokens, sizeof(int32_t) * (C + 3)));
+    HIP_OK(hipMemset(e.tokens, 0, sizeof(int32_t) * (C + 3)));
+    e.start = e.tokens + C;
+    e.last = e.start + 1;
+    e.next = e.last + 1;
+    Q4_OK_OR_DIE(q4llm_step_workspace_bytes(&model, C, L, &e.ws_bytes));
+    HIP_OK(hipMalloc(&e.ws, e.ws_bytes));
+    HIP_OK(hipMemset(e.ws, 0, e.ws_bytes));
+    raw_step(e);  // first launch outside capture: code objects and LDS attributes are set up here
+    HIP_OK(hipStreamSynchronize(stream));
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    raw_step(e);
+    HIP_OK(hipStreamEndCapture(stream, &g));
+    HIP_OK(hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0));
+    HIP_OK(hipGraphDestroy(g));
+    return eps.emplace(key, e).first->second;
+  }
+
+  // One call of the entry point: token ids, start and last in, the greedy next token out.
+  int32_t call(int C, int L, const int32_t* tokens, int n, int start, int last) {
+    EntryPoint& e = entry(C, L);
+    if (C + 3 > host_cap) {
+      if (host) HIP_OK(hipHostFree(host));
+      host_cap = C + 3;
+      HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&host), sizeof(int32_t) * host_cap, hipHostMallocDefault));
+    }
+    for (int i = 0; i < C; ++i) host[i] = i < n ? tokens[i] : 0;
+    host[C] = start;
+    host[C + 1] = last;
+    HIP_OK(hipMemcpyAsync(e.tokens, host, sizeof(int32_t) * (C + 2), hipMemcpyHostToDevice, stream));
+    HIP_OK(hipGraphLaunch(e.exec, stream));
+    HIP_OK(hipMemcpyAsync(host + C + 2, e.next, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
+    HIP_OK(hipStreamSynchronize(stream));
+    return host[C + 2];
+  }
+};
+
+void print_plan(const Plan& p) {
+  std::printf("{\"prefill\":[");
+  for (size_t i = 0; i < p.prefill.size(); ++i) std::printf("%s%d", i ? "," : "", p.prefill[i]);
+  std::printf("],\"decode\":[");
+  for (size_t i = 0; i < p.decode.size(); ++i) std::printf("%s%d", i ? "," : "", p.decode[i]);
+  std::printf("]}\n");
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const Flags f = parse_flags(argc, argv);
+  if (f.prompt.empty()) die("--prompt is required");
+  std::vector<int32_t> buckets = parse_ints(f.buckets);
+  if (buckets.empty()) die("--buckets is empty");
+  for (size_t i = 1; i < buckets.size(); ++i)
+    if (buckets[i] <= buckets[i - 1]) die("--buckets must be ascending (%s)", f.buckets.c_str());
+  const std::vector<int32_t> stops = parse_ints(f.stop_ids);
+  const bool use_max = f.schedule == "max";
+  const std::vector<int32_t> prompt = parse_ints(read_file(f.prompt));
+  const int n_prompt = static_cast<int>(prompt.size());
+  const int C = f.chunk;
+
+  if (f.plan) {  // schedule only: no weights, no GPU
+    const int max_ctx = f.max_ctx > 0 ? f.max_ctx : 4096;  // the reference flag default (llm_runner.c:42)
+    print_plan(make_plan(n_prompt, f.max_new_tokens, C, buckets, max_ctx, use_max));
+    return 0;
+  }
+  if (f.weights.empty()) die("--weights is required");
+
+  Packed pk;
+  load_packed(f.weights, &pk);
+  auto cfg = [&](const char* k) { return static_cast<int>(pk.ints.at(k)); };
+  auto agree = [&](int flag, const char* name, int value) {
+    if (flag > 0 && flag != value) die("--%s=%d disagrees with the weights file (%d there)", name, flag, value);
+  };
+  agree(f.n_layers, "n_layers", cfg("n_layers"));
+  agree(f.n_kv_heads, "n_kv_heads", cfg("n_kv"));
+  agree(f.head_dim, "head_dim", cfg("head_dim"));
+  agree(f.max_ctx, "max_ctx", cfg("max_ctx"));
+  const Plan plan = make_plan(n_prompt, f.max_new_tokens, C, buckets, cfg("max_ctx"), use_max);
+  if (buckets.back() > cfg("max_ctx")) die("bucket %d exceeds max_ctx %d", buckets.back(), cfg("max_ctx"));
+
+  Runner r;
+  const int nl = cfg("n_layers");
+  r.layers.resize(nl);
+  for (int i = 0; i < nl; ++i) {
+    const std::string p = "layers." + std::to_string(i) + ".";
+    q4llm_layer& ly = r.layers[i];
+    ly.wqkv_q = static_cast<const int32_t*>(need(pk, p + "wqkv.qweight"));
+    ly.wqkv_s = static_cast<const uint16_t*>(need(pk, p + "wqkv.scales"));
+    ly.wo_q = static_cast<const int32_t*>(need(pk, p + "wo.qweight"));
+    ly.wo_s = static_cast<const uint16_t*>(need(pk, p + "wo.scales"));
+    ly.wgu_q = static_cast<const int32_t*>(need(pk, p + "wgu.qweight"));
+    ly.wgu_s = static_cast<const uint16_t*>(need(pk, p + "wgu.scales"));
+    ly.wdown_q = static_cast<const int32_t*>(need(pk, p + "wdown.qweight"));
+    ly.wdown_s = static_cast<const uint16_t*>(need(pk, p + "wdown.scales"));
+    ly.ln_in = static_cast<const float*>(need(pk, p + "ln_in"));
+    ly.ln_post = static_cast<const float*>(need(pk, p + "ln_post"));
+  }
+  q4llm_model& m = r.model;
+  m.dim = cfg("dim");
+  m.n_layers = nl;
+  m.n_heads = cfg("n_heads");
+  m.n_kv = cfg("n_kv");
+  m.head_dim = cfg("head_dim");
+  m.inter = cfg("inter");
+  m.vocab = cfg("vocab");
+  m.group = cfg("group");
+  m.max_ctx = cfg("max_ctx");
+  m.eps = pk.eps;
+  m.embed_q = static_cast<const int32_t*>(need(pk, "embed.qweight"));
+  m.embed_s = static_cast<const uint16_t*>(need(pk, "embed.scales"));
+  m.ln_f = static_cast<const float*>(need(pk, "ln_f"));
+  m.cos_t = static_cast<const float*>(need(pk, "cos"));
+  m.sin_t = static_cast<const float*>(need(pk, "sin"));
+  m.layers = r.layers.data();
+
+  // KV caches: zeroed device buffers kept for the whole run (llm_runner.c:301-315).
+  const size_t cache_bytes = static_cast<size_t>(m.max_ctx) * m.n_kv * m.head_dim * 2;
+  r.caches.resize(2 * nl);
+  for (auto& c : r.caches) {
+    HIP_OK(hipMalloc(&c, cache_bytes));
+    HIP_OK(hipMemset(c, 0, cache_bytes));
+  }
+  HIP_OK(hipStreamCreate(&r.stream));
+
+  // Warm-up of every entry point the schedule uses (graph capture included), outside the timings.
+  // The calls write garbage KV at [0, C) that prefill overwrites before anything reads it.
+  const std::vector<int32_t> zeros(C, 0);
+  const double tw = now_ms();
+  std::vector<int> used_pre(plan.prefill), used_dec(plan.decode);
+  for (int w = 0; w < f.warmup; ++w) {
+    for (int L : buckets) {
+      for (int u : used_pre)
+        if (u == L) {
+          r.call(C, L, zeros.data(), C, 0, 0);
+          break;
+        }
+      for (int u : used_dec)
+        if (u == L) {
+          r.call(1, L, zeros.data(), 1, 0, 0);
+          break;
+        }
+    }
+  }
+  const double warm_ms = now_ms() - tw;
+
+  // Prefill (chunked, last chunk zero padded).
+  std::vector<std::pair<int, double>> chunks, steps;
+  std::vector<int32_t> generated;
+  int32_t next = 0;
+  const double t0 = now_ms();
+  for (int start = 0, i = 0; start < n_prompt; start += C, ++i) {
+    const int n = std::min(C, n_prompt - start);
+    const double tc = now_ms();
+    next = r.call(C, plan.prefill[i], prompt.data() + start, n, start, n - 1);
+    chunks.emplace_back(plan.prefill[i], now_ms() - tc);
+  }
+  const double prefill_ms = now_ms() - t0;
+
+  // Decode: the first token comes from prefill.
+  generated.push_back(next);
+  const double t1 = now_ms();
+  int pos = n_prompt;
+  while (static_cast<int>(generated.size()) < f.max_new_tokens) {
+    bool stop = false;
+    for (int s : stops) stop = stop || next == s;
+    if (stop) break;
+    const int L = pick_bucket(buckets, pos + 1, use_max);
+    if (L < 0) break;
+    const double ts = now_ms();
+    const int32_t tok = next;
+    next = r.call(1, L, &tok, 1, pos, 0);
+    steps.emplace_back(L, now_ms() - ts);
+    generated.push_back(next);
+    ++pos;
+  }
+  const double decode_ms = now_ms() - t1;
+  const int n_steps = static_cast<int>(generated.size()) - 1;
+
+  std::printf("{\"schedule\":\"%s\",\"chunk\":%d,\"prompt_tokens\":%d,\"new_tokens\":%d,", f.schedule.c_str(), C,
+              n_prompt, static_cast<int>(generated.size()));
+  std::printf("\"warmup_ms\":%.1f,\"prefill_ms\":%.1f,\"prefill_tok_s\":%.2f,\"ttft_ms\":%.1f,", warm_ms, prefill_ms,
+              n_prompt / (prefill_ms / 1e3), prefill_ms);
+  std::printf("\"decode_ms\":%.1f,\"decode_steps\":%d,\"decode_tok_s\":%.2f,", decode_ms, n_steps,
+              n_steps > 0 ? n_steps / (decode_ms / 1e3) : 0.0);
+  std::printf("\"chunks\":[");
+  for (size_t i = 0; i < chunks.size(); ++i) std::printf("%s[%d,%.1f]", i ? "," : "", chunks[i].first, chunks[i].second);
+  std::printf("],\"steps\":[");
+  for (size_t i = 0; i < steps.size(); ++i) std::printf("%s[%d,%.2f]", i ? "," : "", steps[i].first, steps[i].second);
+  std::printf("],\"tokens\":[");
+  for (size_t i = 0; i < generated.size(); ++i) std::printf("%s%d", i ? "," : "", generated[i]);
+  std::printf("]}\n");
+  std::fflush(stdout);
+
+  for (auto& kv : r.eps) {
+    HIP_OK(hipGraphExecDestroy(kv.second.exec));
+    HIP_OK(hipFree(kv.second.ws));
+    HIP_OK(hipFree(kv.second.tokens));
+  }
+  for (void* c : r.caches) HIP_OK(hipFree(c));
+  for (void* d : pk.device_buffers) HIP_OK(hipFree(d));
+  if (r.host) HIP_OK(hipHostFree(r.host));
+  HIP_OK(hipStreamDestroy(r.stream));
+  return 0;
+}

@@ -206,12 +206,78 @@ class LlamaQ4(nn.Module):
         self.ln_f = nn.Parameter(sd["model.norm.weight"].to(device=device, dtype=torch.float32).contiguous(),
                                  requires_grad=False)
         cos, sin = rope_tables(cfg, max_ctx)
-        self.register_buffer("cos", cos.to(device).contiguous(), persistent=False)
-        self.register_buffer("sin", sin.to(device).contiguous(), persistent=False)
+        self._finish(cos, sin)
+
+    def _finish(self, cos, sin):
+        self.register_buffer("cos", cos.to(self.device).contiguous(), persistent=False)
+        self.register_buffer("sin", sin.to(self.device).contiguous(), persistent=False)
         self._desc = None
         self._ws = {}
         self._io = None
         self._graphs = {}
+
+    # ---------------------------------------------------------------- packed weights
+
+    def packed_config(self):
+        return dict(dim=self.dim, n_layers=self.n_layers, n_heads=self.n_heads, n_kv=self.n_kv,
+                    head_dim=self.head_dim, inter=self.inter, vocab=self.embed.vocab, group=self.group,
+                    max_ctx=self.max_ctx, eps=self.eps)
+
+    def packed_tensors(self):
+        """The device tensors of the model by packed-file name (q4llm.packed)."""
+        t = {"embed.qweight": self.embed.qweight, "embed.scales": self.embed.scales, "ln_f": self.ln_f,
+             "cos": self.cos, "sin": self.sin}
+        for i, ly in enumerate(self.layers):
+            for nm in ("wqkv", "wo", "wgu", "wdown"):
+                q = getattr(ly, nm)
+                t[f"layers.{i}.{nm}.qweight"] = q.qweight
+                t[f"layers.{i}.{nm}.scales"] = q.scales
+            t[f"layers.{i}.ln_in"] = ly.ln_in
+            t[f"layers.{i}.ln_post"] = ly.ln_post
+        return t
+
+    def save_packed(self, path):
+        """Write the quantized model in the packed-weight format (the counterpart of the reference's
+        weights.irpa, export_llama.py:30-31); returns the file size in bytes."""
+        from . import packed
+        return packed.write(path, self.packed_config(), self.packed_tensors())
+
+    @classmethod
+    def from_packed(cls, path, device=None, vocab_chunk=32064):
+        """Load a model written by save_packed: plain copies to the device, no quantization pass."""
+        from . import packed
+        device = _device(device)
+        pc, t = packed.read(path)
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.device = device
+        self.cfg = dict(hidden_size=pc["dim"], num_hidden_layers=pc["n_layers"], num_attention_heads=pc["n_heads"],
+                        num_key_value_heads=pc["n_kv"], head_dim=pc["head_dim"], intermediate_size=pc["inter"],
+                        vocab_size=pc["vocab"], rms_norm_eps=pc["eps"], tie_word_embeddings=True)
+        self.n_layers, self.dim, self.n_heads, self.n_kv = pc["n_layers"], pc["dim"], pc["n_heads"], pc["n_kv"]
+        self.head_dim, self.inter, self.eps = pc["head_dim"], pc["inter"], pc["eps"]
+        self.max_ctx, self.group = pc["max_ctx"], pc["group"]
+        g = self.group
+
+        def dev(name):
+            return t[name].to(device).contiguous()
+
+        self.embed = QEmbedding(group=g, chunk_rows=vocab_chunk, qweight=dev("embed.qweight"),
+                                scales=dev("embed.scales"))
+        layers = []
+        for i in range(self.n_layers):
+            ly = Layer.__new__(Layer)
+            nn.Module.__init__(ly)
+            for nm in ("wqkv", "wo", "wgu", "wdown"):
+                setattr(ly, nm, QLinear(group=g, qweight=dev(f"layers.{i}.{nm}.qweight"),
+                                        scales=dev(f"layers.{i}.{nm}.scales")))
+            ly.ln_in = nn.Parameter(dev(f"layers.{i}.ln_in"), requires_grad=False)
+            ly.ln_post = nn.Parameter(dev(f"layers.{i}.ln_post"), requires_grad=False)
+            layers.append(ly)
+        self.layers = nn.ModuleList(layers)
+        self.ln_f = nn.Parameter(dev("ln_f"), requires_grad=False)
+        self._finish(t["cos"], t["sin"])
+        return self
 
     # ---------------------------------------------------------------- C-ABI descriptor / workspace
 
