@@ -298,8 +298,19 @@ def bench_e2e(dev, n_new=256):
         "buckets_used": sorted({L for L, _ in res["steps"]}),
     }
     log(f"e2e decode {tok_s:.1f} tok/s (GPU-only {1e3 / gpu_ms:.1f}), prefill {res['prefill_tok_s']:.0f} tok/s")
-    del model, caches
-    torch.cuda.empty_cache()
+    # the same generation through the native runner (lib/llm-runner) from the packed weights
+    import tempfile
+    from q4llm import sweep
+    with tempfile.TemporaryDirectory() as td:
+        wpath = pathlib.Path(td) / "llama32_3b_shape.q4w"
+        model.save_packed(wpath)
+        del model, caches
+        torch.cuda.empty_cache()
+        nat = sweep.run_runner(wpath, prompt, n_new, 256, ",".join(map(str, buckets)), "bucketed")
+    out.update(native_runner_decode_tok_s=nat["decode_tok_s"], native_runner_prefill_tok_s=nat["prefill_tok_s"],
+               native_runner_ttft_ms=nat["ttft_ms"], native_runner_tokens_match=nat["tokens"] == res["tokens"])
+    log(f"e2e native runner: decode {nat['decode_tok_s']:.1f} tok/s, prefill {nat['prefill_tok_s']:.0f} tok/s, "
+        f"tokens match: {nat['tokens'] == res['tokens']}")
     return out, res["tokens"]
 
 

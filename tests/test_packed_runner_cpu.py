@@ -90,3 +90,28 @@ def test_native_plan_matches_runner_schedule(tmp_path, n, new, chunk, buckets, m
 def test_native_runner_errors_exit_1(tmp_path, n, flags, msg):
     r = _plan(tmp_path, n, *flags)
     assert r.returncode == 1 and msg in r.stderr, (r.returncode, r.stderr)
+
+
+def test_sweep_summary_medians_and_speedups():
+    from q4llm import sweep
+    recs = []
+    for tag, sched, f in (("run", "bucketed", 1.0), ("run", "max", 0.5)):
+        for ctx in (256, 512):
+            for kind, k in (("a", 1.0), ("b", 3.0), ("c", 2.0)):
+                recs.append(dict(tag=tag, schedule=sched, ctx=ctx, kind=kind, prefill_tok_s=1000 * k * f,
+                                 ttft_ms=10 * k, decode_tok_s=100 * k * f))
+    rows = sweep.summarize(recs)
+    assert [(r["tag"], r["schedule"], r["ctx"]) for r in rows] == [
+        ("run", "bucketed", 256), ("run", "bucketed", 512), ("run", "max", 256), ("run", "max", 512)]
+    assert rows[0]["prefill_tok_s"] == 2000 and rows[0]["decode_tok_s"] == 200 and rows[0]["ttft_s"] == 0.02
+    t = sweep.table(rows).splitlines()
+    assert t[2].endswith("| 1.00 | 1.00 |") and t[4].endswith("| 0.50 | 0.50 |")
+
+
+def test_sweep_prompts(tmp_path):
+    from q4llm import sweep
+    a = sweep.make_prompt("random", 300, 1024, {})
+    assert a == sweep.make_prompt("random", 300, 1024, {}) and len(a) == 300 and max(a) < 1024
+    f = tmp_path / "chat.txt"
+    f.write_text("5 6 7")
+    assert sweep.make_prompt("chat", 7, 1024, {"chat": f}) == [5, 6, 7, 5, 6, 7, 5]

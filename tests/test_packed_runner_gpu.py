@@ -78,3 +78,20 @@ def test_native_runner_ragged_prompt_stop_ids_and_max_schedule(packed_file, tmp_
     res3 = run_native(p, prompt, tmp_path, "--max_new_tokens=10", "--chunk=8", "--buckets=16,32,64",
                       "--schedule=max")
     assert res3["tokens"] == py["tokens"] and {L for L, _ in res3["steps"]} == {64}
+
+
+def test_context_sweep_records(packed_file, tmp_path):
+    """q4llm.sweep (scripts/llm/bench.py:69-107 contract): one record per (kind, ctx, schedule) with
+    the runner's keys plus kind/ctx/tag, and the summary table over them."""
+    from q4llm import sweep
+    p, _ = packed_file
+    out = tmp_path / "sweep.jsonl"
+    assert sweep.main(["run", f"--weights={p}", f"--out={out}", "--ctx", "48", "96", "--new", "8", "--chunk", "16",
+                       "--buckets", "64,128", "--schedule", "bucketed", "max", "--tag", "t"]) == 0
+    recs = [json.loads(line) for line in out.read_text().splitlines()]
+    assert [(r["ctx"], r["schedule"]) for r in recs] == [(48, "bucketed"), (48, "max"), (96, "bucketed"), (96, "max")]
+    assert all(r["prompt_tokens"] == r["ctx"] - 8 and r["new_tokens"] == 8 for r in recs)
+    assert {L for L, _ in recs[0]["steps"]} == {64} and {L for L, _ in recs[1]["steps"]} == {128}
+    assert recs[0]["tokens"] == recs[1]["tokens"]  # the schedule changes buckets, not results
+    rows = sweep.summarize(recs)
+    assert len(rows) == 4 and "| t/bucketed | 48 |" in sweep.table(rows)
