@@ -1,7 +1,7 @@
 """Benchmark of the MI355X int4 LLM hot path (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-e2e] [--skip-cpu] [--skip-gemm]
-                    [--skip-attn] [--sweep-gemv]
+                    [--skip-attn] [--skip-native] [--sweep-gemv]
 
 Headline (the JSON line's `value`): BASELINE config 2, the int4 decode GEMV y = W x at N=5120,
 K=3072 (fused qkv), group 128, fp16 x / fp16 y, fp32 accumulation, in achieved HBM GB/s. A step is
@@ -180,11 +180,11 @@ GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 
                (4096, 4096, 4096), (1, 3072, 3072)]
 
 
-def bench_gemm(dev):
+def bench_gemm(dev, shapes=GEMM_SHAPES):
     import torch
     from q4llm import ops, synth
     out = {}
-    for (M, N, K) in GEMM_SHAPES:
+    for (M, N, K) in shapes:
         a, b = synth.gemm_problem(M, N, K, seed=0)
         A = torch.from_numpy(a).to(dev)
         B0 = torch.from_numpy(b).to(dev)
@@ -248,7 +248,7 @@ LAYER_BYTES_3B = 51_904_512     # wqkv + wo + wgu + wdown packed weights + fp16 
 LM_HEAD_BYTES_3B = 203_157_504  # tied int4 embedding as the LM head
 
 
-def bench_e2e(dev, n_new=256):
+def bench_e2e(dev, n_new=256, native=True):
     import torch
     from q4llm import llm_runner, synth
     from q4llm.llama_q4 import LlamaQ4
@@ -298,6 +298,10 @@ def bench_e2e(dev, n_new=256):
         "buckets_used": sorted({L for L, _ in res["steps"]}),
     }
     log(f"e2e decode {tok_s:.1f} tok/s (GPU-only {1e3 / gpu_ms:.1f}), prefill {res['prefill_tok_s']:.0f} tok/s")
+    if not native:
+        del model, caches
+        torch.cuda.empty_cache()
+        return out, res["tokens"]
     # the same generation through the native runner (lib/llm-runner) from the packed weights
     import tempfile
     from q4llm import sweep
@@ -323,7 +327,11 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attn", action="store_true")
+    ap.add_argument("--skip-native", action="store_true",
+                    help="skip the native-runner e2e leg (a child process: leave it out under a profiler)")
     ap.add_argument("--sweep-gemv", action="store_true", help="time every GEMV tile config (tuning)")
+    ap.add_argument("--gemm-shapes", nargs="*", default=None, metavar="MxNxK",
+                    help="run the GEMM leg on these shapes only (default: every config-3 shape)")
     ap.add_argument("--tokens-out", default=None, help="write the e2e generated token ids here")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -393,11 +401,13 @@ def main():
         "measured_probes": probes,
     }
     if not a.skip_gemm:
-        out["gemm_f16"] = bench_gemm(dev)
+        shapes = ([tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes] if a.gemm_shapes is not None
+                  else GEMM_SHAPES)
+        out["gemm_f16"] = bench_gemm(dev, shapes)
     if not a.skip_attn:
         out["attn_decode"] = bench_attn(dev)
     if not a.skip_e2e:
-        e2e, tokens = bench_e2e(dev)
+        e2e, tokens = bench_e2e(dev, native=not a.skip_native)
         out["e2e_3b"] = e2e
         if a.tokens_out:
             pathlib.Path(a.tokens_out).write_text(json.dumps(tokens))
