@@ -132,6 +132,17 @@ int q4_gemv_epilogue(const int32_t* qweight, const uint16_t* scales, const float
 int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
               const float* residual, int64_t N, int64_t K, int group, void* stream);
 
+/* Workspace bytes q4_linear_ws needs for M rows of K: the fp16 hi and lo planes of x (4 * M * K). */
+int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes);
+
+/* q4_linear (QLinear.forward at M > 1, llama_q4.py:72) with a caller workspace: x is split once into
+ * fp16 hi/lo planes in `workspace`, then a multi-stage matrix-core pipeline streams both planes and
+ * the packed int4 weights (two launches on `stream`). Same contract and accuracy as q4_linear;
+ * workspace >= q4_linear_workspace_bytes(M, K), 16-byte aligned. */
+int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
+                 const float* residual, int64_t N, int64_t K, int group, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
 /* fp16 GEMM C[M,N] = A[M,K] @ B[N,K]^T ("NT", gemm/shapes.py:4-6, S2 prefill_nt), fp32
  * accumulation, fp16 output, row-major with leading dimensions lda/ldb/ldc (in elements).
  * M == 1 runs a memory-bound fp16 GEMV. Requires K % 8 == 0, lda/ldb % 8 == 0, 16-byte aligned

@@ -237,6 +237,311 @@ using LinFn = void (*)(const float*, const int32_t*, const uint16_t*, float*, co
 constexpr LinFn kLinFns[] = {q4_linear_kernel<128, 128>, q4_linear_kernel<128, 64>, q4_linear_kernel<64, 64>};
 constexpr size_t kLinLds[] = {LinCfg<128, 128>::kLds, LinCfg<128, 64>::kLds, LinCfg<64, 64>::kLds};
 
+// ------------------------------------------------------------------------------------------------
+// Workspace variant (q4_linear_ws): x is split once per call, then a multi-stage MFMA pipeline.
+//
+//   * split_x_kernel writes x_hi = fp16(x) and x_lo = fp16(x - x_hi) as two [M, K] fp16 planes, each
+//     8-element chunk stored in the order (0, 4, 1, 5, 2, 6, 3, 7);
+//   * the weight operand is decoded in registers straight from the packed word: the masks
+//     (w >> 4i) & 0x000F000F | 0x64006400 make the fp16 pair (1024 + n_i, 1024 + n_{i+4}) and one
+//     packed fp16 add of -1032 gives (n - 8) exactly, in the same (0, 4, 1, 5, ...) order, so the
+//     MFMA's k products pair up with the x planes (the order of k inside one MFMA does not matter);
+//   * x_hi, x_lo and the packed weights stream into an NST-stage LDS ring with direct global -> LDS
+//     16-byte loads (the fp16 GEMM's pipeline; x rows use its conflict-free swizzle), so no VGPRs
+//     stage data and NST-1 K steps are in flight;
+//   * per 16-k step two MFMAs (x_hi, x_lo) accumulate a group partial in fp32; at each group end the
+//     partial is scaled by the fp32 group scale (loaded one K step ahead) into the output.
+// ------------------------------------------------------------------------------------------------
+
+constexpr uint32_t kOOBw = 0x80000000u;
+
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 16, off, 0, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One thread per 8-element chunk of x: two 16-byte loads, two 16-byte stores.
+__global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ x, uint16_t* __restrict__ xh,
+                                                      uint16_t* __restrict__ xl, int64_t chunks) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const float4 a = reinterpret_cast<const float4*>(x)[2 * c];
+  const float4 b = reinterpret_cast<const float4*>(x)[2 * c + 1];
+  const float v[8] = {a.x, b.x, a.y, b.y, a.z, b.z, a.w, b.w};  // order 0, 4, 1, 5, 2, 6, 3, 7
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const _Float16 h0 = static_cast<_Float16>(v[2 * p]), h1 = static_cast<_Float16>(v[2 * p + 1]);
+    const _Float16 l0 = static_cast<_Float16>(v[2 * p] - static_cast<float>(h0));
+    const _Float16 l1 = static_cast<_Float16>(v[2 * p + 1] - static_cast<float>(h1));
+    h[p] = __builtin_bit_cast(uint16_t, h0) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+    l[p] = __builtin_bit_cast(uint16_t, l0) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+  }
+  reinterpret_cast<uint4*>(xh)[c] = make_uint4(h[0], h[1], h[2], h[3]);
+  reinterpret_cast<uint4*>(xl)[c] = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Packed word of 8 nibbles (k = 8c + b at nibble b) -> the fp16 operand (n_b - 8) in k order
+// (0, 4, 1, 5, 2, 6, 3, 7). Exact: 1024 + n is an fp16 integer and so is n - 8.
+__device__ __forceinline__ half8 nibbles_to_half8(uint32_t w) {
+  const half2v bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+  half2v p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    p[i] = __builtin_bit_cast(half2v, ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u) + bias;
+  return half8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+}
+
+// Wait until this wave's loads of the stage being consumed have landed: `after` later stages (LPW
+// loads each) and `sc` later scale batches (SPW loads each) may stay in flight. vmcnt needs an
+// immediate, so the (after, sc) pairs are dispatched to constants.
+template <int LPW, int SPW, int A, int S>
+__device__ __forceinline__ void wait_case(int after, int sc) {
+  if (after == A && sc == S) wait_vmcnt<A * LPW + S * SPW>();
+}
+template <int LPW, int SPW, int NST>
+__device__ __forceinline__ void wait_stage(int after, int sc) {
+  wait_case<LPW, SPW, 0, 0>(after, sc);
+  wait_case<LPW, SPW, 0, 1>(after, sc);
+  if constexpr (NST >= 3) {
+    wait_case<LPW, SPW, 0, 2>(after, sc);
+    wait_case<LPW, SPW, 1, 0>(after, sc);
+    wait_case<LPW, SPW, 1, 1>(after, sc);
+    wait_case<LPW, SPW, 1, 2>(after, sc);
+  }
+  if constexpr (NST >= 4) {
+    wait_case<LPW, SPW, 0, 3>(after, sc);
+    wait_case<LPW, SPW, 1, 3>(after, sc);
+    wait_case<LPW, SPW, 2, 0>(after, sc);
+    wait_case<LPW, SPW, 2, 1>(after, sc);
+    wait_case<LPW, SPW, 2, 2>(after, sc);
+    wait_case<LPW, SPW, 2, 3>(after, sc);
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int NST>
+struct LinWsCfg {
+  static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
+  static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  static constexpr int kXRow = 128;                        // bytes per x row per stage (64 fp16)
+  static constexpr int kWRow = 32;                         // bytes per weight row per stage (64 nibbles)
+  static constexpr int kStage = 2 * BM * kXRow + BN * kWRow;
+  static constexpr int kAI = BM / 8 / kWaves;             // x direct loads per wave, per plane
+  static constexpr int kBI = (BN / 32 + kWaves - 1) / kWaves;  // weight direct loads per wave (32 rows each)
+  static constexpr int kLPW = 2 * kAI + kBI;
+  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + 1024;  // + junk for spare weight loads
+  static_assert(TM >= 1 && TN >= 1 && kAI * 8 * kWaves == BM, "tile shape");
+  static constexpr int kSPW = 2 * TN;                      // scale loads per wave per K step
+  static_assert(NST >= 2 && NST <= 4 && kLPW * (NST - 2) + kSPW * (NST - 1) < 64, "stages");
+};
+
+template <int BM, int BN, int WM, int WN, int NST>
+__global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
+    const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
+    const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n) {
+  using G = LinWsCfg<BM, BN, WM, WN, NST>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int spr = K / group;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const uint32_t xbytes = static_cast<uint32_t>(M) * K * 2u;
+  const __amdgpu_buffer_rsrc_t hr = make_rsrc(XH, xbytes);
+  const __amdgpu_buffer_rsrc_t lr = make_rsrc(XL, xbytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(QW, static_cast<uint32_t>(N) * (K / 2));
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(SC, (static_cast<uint32_t>(N) * spr * 2u + 3u) & ~3u);
+
+  // x planes: instruction j fills rows 8b..8b+7 (b = wave + j * kWaves) of a 128-byte-row plane; the
+  // lane for slot (lane % 8) of row r = 8b + lane / 8 fetches chunk (lane % 8) ^ ((r >> 1) & 7).
+  uint32_t xoff[G::kAI];
+  int xchunk[G::kAI];
+#pragma unroll
+  for (int j = 0; j < G::kAI; ++j) {
+    const int r = 8 * (wave + j * G::kWaves) + (lane >> 3);
+    xchunk[j] = (lane & 7) ^ ((r >> 1) & 7);
+    xoff[j] = m0 + r < M ? static_cast<uint32_t>(m0 + r) * K * 2u + xchunk[j] * 16u : kOOBw;
+  }
+  // weights: instruction j fills rows 32b..32b+31 (b = wave + j * kWaves < BN / 32) with 32-byte rows,
+  // lane -> (row lane / 2, half lane % 2); spare instructions load nothing into a junk area.
+  uint32_t woff[G::kBI];
+  bool wreal[G::kBI];
+#pragma unroll
+  for (int j = 0; j < G::kBI; ++j) {
+    const int b = wave + j * G::kWaves;
+    const int r = 32 * b + (lane >> 1);
+    wreal[j] = b < BN / 32;
+    woff[j] = wreal[j] && n0 + r < N ? static_cast<uint32_t>(n0 + r) * (K / 2) + (lane & 1) * 16u : kOOBw;
+  }
+  unsigned char* junk = lds + NST * G::kStage;
+  // Every step issues the same loads (steps past K load zeros into a free stage), so the number of
+  // vector-memory operations in flight is the same on every path: the exact waits below and the
+  // compiler's own waits for the scale registers then agree.
+  auto issue = [&](int kt, int stage) {
+    const int k0 = kt * 64;
+    const bool kin = k0 < K;
+    unsigned char* sh = lds + stage * G::kStage;
+    unsigned char* sl = sh + BM * G::kXRow;
+    unsigned char* sw = sl + BM * G::kXRow;
+#pragma unroll
+    for (int j = 0; j < G::kAI; ++j) {
+      const uint32_t off = kin && xoff[j] != kOOBw ? xoff[j] + k0 * 2u : kOOBw;
+      load_lds16(hr, sh + (wave + j * G::kWaves) * 1024, off);
+      load_lds16(lr, sl + (wave + j * G::kWaves) * 1024, off);
+    }
+#pragma unroll
+    for (int j = 0; j < G::kBI; ++j)
+      load_lds16(wr, wreal[j] ? sw + (wave + j * G::kWaves) * 1024 : junk,
+                 kin && woff[j] != kOOBw ? woff[j] + k0 / 2 : kOOBw);
+  };
+
+  // Scales of the groups in K step kt for this lane's TN columns (2 slots: a 64-k step touches at
+  // most two groups of >= 32), loaded one K step ahead as the aligned dword holding the fp16 value
+  // (the buffer range is rounded up to 4 bytes; device allocations are 256-byte granular). No
+  // conditions: a column past N lies past the end of the scales (the range check returns zeros),
+  // and the prefetch past the last step reads an unused in-range value or zeros.
+  auto scale_elem = [&](int j, int g) -> uint32_t {
+    const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+    return static_cast<uint32_t>(col) * spr + g;
+  };
+  auto scale_load = [&](int kt, uint32_t (&s)[2][G::TN]) {
+    const int g0 = (kt * 64) / group, g1 = (kt * 64 + 63) / group;
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j) {
+      s[0][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(sr, (scale_elem(j, g0) >> 1) * 4u, 0, 0));
+      s[1][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(sr, (scale_elem(j, g1) >> 1) * 4u, 0, 0));
+    }
+  };
+  auto scale_of = [&](const uint32_t (&s)[2][G::TN], int slot, int j, int g) {
+    return half_bits_to_float(static_cast<uint16_t>(s[slot][j] >> (16 * (scale_elem(j, g) & 1))));
+  };
+
+  float16v acc[G::TM][G::TN], part[G::TM][G::TN];
+#pragma unroll
+  for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = part[i][j][e] = 0.0f;
+
+  const int arow = wm * G::WTM + (lane & 31);
+  const int brow = wn * G::WTN + (lane & 31);
+  const int nk = K / 64;
+  // Load order per wave: scales of step 0, stages 0..NST-2, then per step kt: the scales of step
+  // kt+1 and stage kt+NST-1. At step kt the loads issued after stage kt are NST-2 stages and
+  // min(kt, NST-2) scale batches (the compiler barriers keep this order). The scale registers
+  // alternate between two sets (the loop is unrolled by two), so no copy waits on a fresh load,
+  // and the newest loads in flight are always stage loads.
+  auto step = [&](int kt, const uint32_t (&scur)[2][G::TN], uint32_t (&snext)[2][G::TN]) {
+    wait_stage<G::kLPW, G::kSPW, NST>(NST - 2, min(kt, NST - 2));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    scale_load(kt + 1, snext);  // past the last step: unused
+    asm volatile("" ::: "memory");
+    issue(kt + NST - 1, (kt + NST - 1) % NST);
+    asm volatile("" ::: "memory");
+    const unsigned char* sh = lds + (kt % NST) * G::kStage;
+    const unsigned char* sl = sh + BM * G::kXRow;
+    const unsigned char* sw = sl + BM * G::kXRow;
+    const int k0 = kt * 64;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = 2 * kk + (lane >> 5);  // this lane's 8-k chunk of the step
+      const int xs = (c ^ ((lane >> 1) & 7)) << 4;
+      half8 fh[G::TM], fl[G::TM], fb[G::TN];
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i) {
+        fh[i] = *reinterpret_cast<const half8*>(sh + (arow + 32 * i) * G::kXRow + xs);
+        fl[i] = *reinterpret_cast<const half8*>(sl + (arow + 32 * i) * G::kXRow + xs);
+      }
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j)
+        fb[j] = nibbles_to_half8(*reinterpret_cast<const uint32_t*>(sw + (brow + 32 * j) * G::kWRow + 4 * c));
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[i], fb[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[i], fb[j], part[i][j], 0, 0, 0);
+        }
+      const int k = k0 + 16 * kk;
+      if ((k + 16) % group == 0) {  // the group ends with this 16-k step: apply its scale
+        const int g = k / group;
+        const int gi = g - k0 / group;
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+          const float sc = scale_of(scur, gi, j, g);
+#pragma unroll
+          for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              acc[i][j][e] = fmaf(part[i][j][e], sc, acc[i][j][e]);
+              part[i][j][e] = 0.0f;
+            }
+        }
+      }
+    }
+  };
+  uint32_t sa[2][G::TN], sb[2][G::TN];
+  scale_load(0, sa);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue(s, s);
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, sa, sb);
+    if (kt + 1 < nk) step(kt + 1, sb, sa);
+  }
+
+#pragma unroll
+  for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+        const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+        if (row < M && col < N) {
+          const int64_t o = static_cast<int64_t>(row) * N + col;
+          Y[o] = R ? R[o] + acc[i][j][e] : acc[i][j][e];
+        }
+      }
+}
+
+struct LinWsTile {
+  int bm, bn, wm, wn, nst;
+};
+// Explicit tile list (index stable for Q4_LINEAR_CFG sweeps).
+constexpr LinWsTile kLinWsTiles[] = {
+    {128, 128, 2, 2, 4},  // 0: 4 waves of 64x64, 4 stages (144 KB)
+    {64, 128, 2, 2, 4},   // 1: 4 waves of 32x64, 4 stages (80 KB)
+    {64, 64, 2, 2, 4},    // 2: 4 waves of 32x32, 4 stages (72 KB)
+    {128, 64, 2, 2, 4},   // 3: 4 waves of 64x32 (104 KB)
+};
+using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
+                         int, int, int, int);
+template <int I>
+constexpr LinWsFn lin_ws_fn() {
+  constexpr LinWsTile t = kLinWsTiles[I];
+  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst>;
+}
+template <int I>
+constexpr size_t lin_ws_lds() {
+  constexpr LinWsTile t = kLinWsTiles[I];
+  return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst>::kLds;
+}
+constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(), lin_ws_fn<3>()};
+constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(), lin_ws_lds<3>()};
+constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
+
 }  // namespace
 
 int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
@@ -261,7 +566,72 @@ int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_
   return launch_status();
 }
 
+// Fixed rule: the largest tile (in list order 0, 3, 1, 2) giving at least 256 workgroups, else the
+// smallest. Q4_LINEAR_CFG overrides for sweeps.
+int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
+                        int64_t N, int64_t K, int group, void* ws, hipStream_t st) {
+  uint16_t* xh = static_cast<uint16_t*>(ws);
+  uint16_t* xl = xh + M * K;
+  const int64_t chunks = M * K / 8;
+  hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, st, x, xh, xl,
+                     chunks);
+  if (int e = launch_status()) return e;
+  int ti = -1;
+  const char* ov = getenv("Q4_LINEAR_CFG");
+  if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
+  if (ti < 0) {
+    ti = 2;
+    for (int i : {0, 3, 1, 2}) {
+      const LinWsTile& t = kLinWsTiles[i];
+      if (((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) >= 256) {
+        ti = i;
+        break;
+      }
+    }
+  }
+  const LinWsTile& t = kLinWsTiles[ti];
+  const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
+  const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
+  if (kLinWsLds[ti] > 64 * 1024) {
+    Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kLinWsFns[ti]),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[ti])));
+  }
+  hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
+                     (int)M, (int)N, (int)K, group, tiles_n);
+  return launch_status();
+}
+
 }  // namespace q4
+
+namespace {
+int linear_args(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y, int64_t N,
+                int64_t K, int group) {
+  if (!x || !qweight || !scales || !y) return Q4_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0 || group <= 0) return Q4_ERR_SHAPE;
+  if (K % 64 || group % 32 || K % group) return Q4_ERR_SHAPE;
+  if (M * K * 4 >= (int64_t{1} << 31) || N * (K / 2) >= (int64_t{1} << 31) || M > INT32_MAX || N > INT32_MAX)
+    return Q4_ERR_SHAPE;
+  if (!q4::aligned(x, 16) || !q4::aligned(qweight, 16) || !q4::aligned(y, 4)) return Q4_ERR_ALIGN;
+  return Q4_OK;
+}
+}  // namespace
+
+extern "C" int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (M <= 0 || K <= 0 || K % 64) return Q4_ERR_SHAPE;
+  *bytes = static_cast<size_t>(M) * static_cast<size_t>(K) * 4;  // x_hi and x_lo planes, fp16
+  return Q4_OK;
+}
+
+extern "C" int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
+                            const float* residual, int64_t N, int64_t K, int group, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (int st = linear_args(x, M, qweight, scales, y, N, K, group)) return st;
+  if (!workspace) return Q4_ERR_NULL;
+  if (workspace_bytes < static_cast<size_t>(M) * static_cast<size_t>(K) * 4) return Q4_ERR_WORKSPACE;
+  if (!q4::aligned(workspace, 16)) return Q4_ERR_ALIGN;
+  return q4::q4_linear_ws_launch(x, M, qweight, scales, y, residual, N, K, group, workspace, q4::as_stream(stream));
+}
 
 extern "C" int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
                          const float* residual, int64_t N, int64_t K, int group, void* stream) {

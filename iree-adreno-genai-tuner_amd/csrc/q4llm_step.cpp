@@ -13,7 +13,7 @@
 // then x = rms_norm(h[last], ln_f), logits = x E^T (tied int4 embedding), next = argmax(logits).
 // Projections: C == 1 -> q4_gemv (fp32 in/out, residual fused; norms, RoPE + cache writes and SwiGLU
 // fused into the GEMVs); C > 1 -> q4_linear (fused int4 MFMA GEMM with split-fp16 activations and
-// per-group fp32 scales, residual fused).
+// per-group fp32 scales, residual fused; its fp16 x planes live in the step workspace).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -24,8 +24,8 @@
 namespace {
 
 struct Layout {
-  size_t h, x, qkv, o, gu, act, xf, logits, attn, amax, total;
-  size_t attn_bytes, amax_bytes;
+  size_t h, x, qkv, o, gu, act, xf, logits, attn, amax, lin, total;
+  size_t attn_bytes, amax_bytes, lin_bytes;
 };
 
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
@@ -50,6 +50,16 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   lo->amax = take(amax);
   lo->attn_bytes = attn;
   lo->amax_bytes = amax;
+  // prefill projections: the fp16 hi/lo planes of their input (largest K of the four)
+  size_t lin = 0;
+  if (C > 1) {
+    int64_t kmax = m->dim;
+    if (nq > kmax) kmax = nq;
+    if (m->inter > kmax) kmax = m->inter;
+    if (int st = q4_linear_workspace_bytes(C, kmax, &lin)) return st;
+  }
+  lo->lin = take(lin);
+  lo->lin_bytes = lin;
   lo->total = off;
   return Q4_OK;
 }
@@ -69,11 +79,11 @@ int check_model(const q4llm_model* m) {
   return Q4_OK;
 }
 
-// y = residual + x W^T for C rows (C == 1: GEMV, else fused int4 GEMM).
+// y = residual + x W^T for C rows (C == 1: GEMV, else the fused int4 GEMM with its x planes in ws).
 int proj(int C, const float* x, const int32_t* q, const uint16_t* s, float* y, const float* res, int N, int K, int group,
-         void* stream) {
+         void* ws, size_t ws_bytes, void* stream) {
   if (C == 1) return q4_gemv(q, s, x, Q4_F32, y, Q4_F32, res, N, K, group, stream);
-  return q4_linear(x, C, q, s, y, res, N, K, group, stream);
+  return q4_linear_ws(x, C, q, s, y, res, N, K, group, ws, ws_bytes, stream);
 }
 
 // The fused decode GEMVs (qkv and gate/up, K = dim) need the vectorised layout: K % 32 == 0,
@@ -118,6 +128,7 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   float* lg = logits ? logits : reinterpret_cast<float*>(ws + lo.logits);
   void* attn_ws = ws + lo.attn;
   void* amax_ws = ws + lo.amax;
+  void* lin_ws = ws + lo.lin;
 
   const int D = m->dim, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv;
   const int nq_w = nh * hd, qkv_w = (nh + 2 * nkv) * hd;
@@ -144,20 +155,20 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
                               qkv_w, D, m->group, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
-      Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, stream));
+      Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, lin_ws, lo.lin_bytes, stream));
       Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     }
     Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
-    Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, stream));
+    Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, lin_ws, lo.lin_bytes, stream));
     if (fused) {
       Q4_TRY(q4_gemv_epilogue(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU, nullptr, act,
                               2 * m->inter, D, m->group, stream));
       Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
-      Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, stream));
+      Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, lin_ws, lo.lin_bytes, stream));
       Q4_TRY(silu_mul_f32(gu, act, C, m->inter, stream));
-      Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, stream));
+      Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, lin_ws, lo.lin_bytes, stream));
     }
   }
   Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));

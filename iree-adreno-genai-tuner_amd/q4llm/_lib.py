@@ -36,6 +36,8 @@ SIGNATURES = {
     "q4_gemv_fused": [p, p, p, i32, p, f32, p, p, i64, i64, i32, p],
     "q4_gemv_epilogue": [p, p, p, i32, p, f32, i32, p, p, i64, i64, i32, p],
     "q4_linear": [p, i64, p, p, p, p, i64, i64, i32, p],
+    "q4_linear_workspace_bytes": [i64, i64, C.POINTER(sz)],
+    "q4_linear_ws": [p, i64, p, p, p, p, i64, i64, i32, p, sz, p],
     "gemm_f16_nt": [p, p, p, i64, i64, i64, i64, i64, i64, p],
     "gemm_f16_nt_cfg": [p, p, p, i64, i64, i64, i64, i64, i64, i32, i32, p],
     "gemm_f16_num_configs": [],

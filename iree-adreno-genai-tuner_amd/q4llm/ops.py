@@ -124,6 +124,23 @@ def q4_linear(x, qweight, scales, group, residual=None, out=None):
     return out
 
 
+def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=None):
+    """q4_linear through the workspace entry point (x split once, multi-stage MFMA pipeline)."""
+    _dev(qweight, scales, x, residual)
+    m, k = x.shape
+    n = qweight.shape[0]
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.float32, device=x.device)
+    b = C.c_size_t(0)
+    LIB.call("q4_linear_workspace_bytes", m, k, C.byref(b))
+    if workspace is None:
+        workspace = torch.empty(b.value, dtype=torch.uint8, device=x.device)
+    LIB.call("q4_linear_ws", ptr(x), m, ptr(qweight), ptr(scales), ptr(out), ptr(residual), n, k, group,
+             ptr(workspace), workspace.numel(), stream_of(x.device))
+    return out
+
+
 def gemm_f16_nt(a, b, out=None):
     """C [M, N] fp16 = A [M, K] @ B [N, K]^T with fp32 accumulation (gemm/shapes.py 'NT')."""
     _dev(a, b)

@@ -154,6 +154,30 @@ def test_q4_linear_fp32_accuracy(dev, M, N, K, group):
     assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
 
 
+@pytest.mark.parametrize("M,N,K,group", [(256, 5120, 3072, 128), (256, 3072, 8192, 128), (16, 1408, 256, 32),
+                                         (16, 256, 704, 32), (7, 100, 128, 64), (300, 3072, 3072, 128),
+                                         (256, 16384, 3072, 128), (33, 200, 320, 64)])
+def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch):
+    """The workspace entry point (x split into fp16 hi/lo planes, multi-stage pipeline) keeps the
+    fp32-level accuracy of q4_linear on every tile of its list, with ragged M and N."""
+    g = torch.Generator().manual_seed(M + N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g)
+    res = torch.randn(M, N, generator=g)
+    qw, sc = R.quantize_q4(w, group)
+    ref = x.double() @ R.dequantize_q4(qw, sc, group).double().T
+    rms = ref.pow(2).mean().sqrt().item()
+    xd, qd, sd = x.to(dev), qw.to(dev), sc.to(dev)
+    for cfg in ("", "0", "1", "2", "3"):
+        monkeypatch.setenv("Q4_LINEAR_CFG", cfg)
+        y = nan_like((M, N), torch.float32, dev)
+        ops.q4_linear_ws(xd, qd, sd, group, out=y)
+        assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms, cfg
+    h = res.to(dev).clone()
+    ops.q4_linear_ws(xd, qd, sd, group, residual=h, out=h)
+    assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
+
+
 # ------------------------------------------------------------------------------------------------
 # support ops
 # ------------------------------------------------------------------------------------------------
