@@ -295,6 +295,302 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / D;
 }
 
+// ---- Decode (one query row): a register-resident split kernel and a merge that needs no position ----
+//
+// Workgroup (split, kv head) of 4 waves covers S = 4 * NK * KPI keys for the G query heads of the
+// group. In each wave, LPK = HD / 8 lanes hold one key (8 dims, one 16-byte load of K and one of V
+// per lane and key), KPI = 64 / LPK keys side by side, NK such rows. Everything up to the wave's
+// partial (m, l, o) stays in registers: scores are summed over the LPK lanes of a key with DPP,
+// the max, the denominator and o are summed over the wave's key groups with the gfx950 lane swaps;
+// one barrier then merges the four waves' partials through LDS. Every reduction is a butterfly in
+// which partners add the same two values, so all lanes hold bit-identical results.
+//
+// Splits wholly past `pos` write m = -inf, l = 0 and o = 0, so the merge reads every split without
+// knowing `pos`. Splits in the first half of the bucket (never empty when the bucket is the
+// smallest one >= pos + 1) issue their K/V loads before `pos` arrives; the others wait for it and
+// load nothing when empty.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the LPK (8 or 16) aligned lanes of a key: row_mirror (i <-> 15 - i), row_half_mirror
+// (i <-> 7 - i in each half row), then quad_perm xor 1 and xor 2 -- the xor masks 15, 7, 1, 2 span
+// the lane index bits, so every lane ends with the full sum.
+template <int LPK>
+__device__ __forceinline__ float key_sum(float v) {
+  if constexpr (LPK == 16) v += dpp<0x140>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  return v;
+}
+
+template <bool kMax>
+__device__ __forceinline__ float combine2(float a, float b) {
+  return kMax ? fmaxf(a, b) : a + b;
+}
+
+// Reduce over the key groups of a wave (lane bits >= log2(LPK)): xor 8 by row_ror:8 (LPK == 8),
+// xor 16 by v_permlane16_swap (odd rows of one copy trade places with even rows of the other),
+// xor 32 by v_permlane32_swap (upper half of one copy with the lower half of the other). The swaps
+// are inline asm: given one value for both operands, this compiler folds the builtins' two results
+// into the first.
+// The s_nop 1 on each side covers the VALU-write -> permlane-read and the DPP-read hazards.
+template <bool kMax>
+__device__ __forceinline__ float swap_combine16(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return combine2<kMax>(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+template <bool kMax>
+__device__ __forceinline__ float swap_combine32(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return combine2<kMax>(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+template <int LPK, bool kMax>
+__device__ __forceinline__ float across_keys(float v) {
+  if constexpr (LPK == 8) v = combine2<kMax>(v, dpp<0x128>(v));
+  return swap_combine32<kMax>(swap_combine16<kMax>(v));
+}
+
+template <int HD, int NK, int G>
+__global__ __launch_bounds__(kThreads) void attn_decode_split_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ ws_ml, float* __restrict__ ws_o, int n_kv, int L, const int32_t* __restrict__ start_p,
+    float scale) {
+  constexpr int LPK = HD / 8, KPI = 64 / LPK, KPW = NK * KPI, S = 4 * KPW;
+  __shared__ float4 red_o[4][G][HD / 4];
+  __shared__ float2 red_ml[4][G];
+  const int split = blockIdx.x, hk = blockIdx.y, n_splits = gridDim.x;
+  const int k0 = split * S;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kg = lane / LPK, d8 = lane % LPK;
+  const int key0 = k0 + wave * KPW + kg;  // key of row i is key0 + i * KPI
+  const uint32_t cache_bytes = static_cast<uint32_t>(L) * n_kv * HD * 2u;
+  const __amdgpu_buffer_rsrc_t kres = make_rsrc(kc, cache_bytes);
+  const __amdgpu_buffer_rsrc_t vres = make_rsrc(vc, cache_bytes);
+  const uint32_t off0 = (static_cast<uint32_t>(key0) * n_kv + hk) * (HD * 2u) + d8 * 16u;
+  const uint32_t row_step = static_cast<uint32_t>(KPI) * n_kv * (HD * 2u);
+
+  // Queries first (independent of everything), then K/V: early splits before `pos` is known.
+  float4 qa[G], qb[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const float4* qp = reinterpret_cast<const float4*>(q + static_cast<size_t>(hk * G + j) * HD + d8 * 8);
+    qa[j] = qp[0];
+    qb[j] = qp[1];
+  }
+  uint4 kreg[NK], vreg[NK];
+  int pos;
+  if (2 * (k0 + S) <= L) {
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      kreg[i] = buf_load16(kres, off0 + i * row_step);
+      vreg[i] = buf_load16(vres, off0 + i * row_step);
+    }
+    pos = start_p[0];
+  } else {
+    pos = start_p[0];
+    const uint32_t dead = k0 > pos ? 0x80000000u : 0u;  // out of range: zeros, no traffic
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      kreg[i] = buf_load16(kres, (off0 + i * row_step) | dead);
+      vreg[i] = buf_load16(vres, (off0 + i * row_step) | dead);
+    }
+  }
+
+  // Scores of the G queries against the wave's keys (identical in the LPK lanes of a key).
+  float s[G][NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    float kf[8];
+    unpack8(kreg[i], kf);
+    const int key = key0 + i * KPI;
+    const bool live = key <= pos && key < L;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      float d = qa[j].x * kf[0];
+      d = fmaf(qa[j].y, kf[1], d);
+      d = fmaf(qa[j].z, kf[2], d);
+      d = fmaf(qa[j].w, kf[3], d);
+      d = fmaf(qb[j].x, kf[4], d);
+      d = fmaf(qb[j].y, kf[5], d);
+      d = fmaf(qb[j].z, kf[6], d);
+      d = fmaf(qb[j].w, kf[7], d);
+      d = key_sum<LPK>(d);
+      s[j][i] = live ? d * scale : -INFINITY;
+    }
+  }
+  // Wave-local softmax statistics and o = sum_k p_k v_k over the wave's keys.
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    float mj = s[j][0];
+#pragma unroll
+    for (int i = 1; i < NK; ++i) mj = fmaxf(mj, s[j][i]);
+    m[j] = across_keys<LPK, true>(mj);
+    float lj = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      s[j][i] = s[j][i] == -INFINITY ? 0.0f : expf(s[j][i] - m[j]);
+      lj += s[j][i];
+    }
+    l[j] = lj;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    float vf[8];
+    unpack8(vreg[i], vf);
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[j][e] = fmaf(s[j][i], vf[e], o[j][e]);
+  }
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    l[j] = across_keys<LPK, false>(l[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = across_keys<LPK, false>(o[j][e]);
+  }
+  if (kg == 0) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      red_o[wave][j][2 * d8] = make_float4(o[j][0], o[j][1], o[j][2], o[j][3]);
+      red_o[wave][j][2 * d8 + 1] = make_float4(o[j][4], o[j][5], o[j][6], o[j][7]);
+    }
+    if (d8 == 0) {
+#pragma unroll
+      for (int j = 0; j < G; ++j) red_ml[wave][j] = make_float2(m[j], l[j]);
+    }
+  }
+  __syncthreads();
+
+  // Merge the four waves: thread -> (query j, 4 dims).
+  for (int e = threadIdx.x; e < G * (HD / 4); e += kThreads) {
+    const int j = e / (HD / 4), d4 = e % (HD / 4);
+    float M = red_ml[0][j].x;
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, red_ml[w][j].x);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float2 ml = red_ml[w][j];
+      const float f = ml.x == -INFINITY ? 0.0f : expf(ml.x - M);
+      const float4 ow = red_o[w][j][d4];
+      acc.x = fmaf(f, ow.x, acc.x);
+      acc.y = fmaf(f, ow.y, acc.y);
+      acc.z = fmaf(f, ow.z, acc.z);
+      acc.w = fmaf(f, ow.w, acc.w);
+      den = fmaf(f, ml.y, den);
+    }
+    const size_t idx = static_cast<size_t>(hk * G + j) * n_splits + split;
+    reinterpret_cast<float4*>(ws_o + idx * HD)[d4] = acc;
+    if (d4 == 0) {
+      ws_ml[2 * idx] = M;
+      ws_ml[2 * idx + 1] = den;
+    }
+  }
+}
+
+// Decode merge over n_splits <= MS (32 or 64) partials of each head: every split's (m, l) and o are
+// read unconditionally (empty splits hold -inf, 0, 0), so there is no dependence on `pos`. Lane j of
+// each wave (and lane j + 32 when MS == 32) loads split j's (m, l); the max and the denominator are
+// butterflies over those lanes, and the weights reach every thread through v_readlane for the
+// numerator, which is summed in ascending split order.
+constexpr int kDecodeMaxSplits = 64;
+
+template <int MS, bool kMax>
+__device__ __forceinline__ float butterfly(float v) {
+  v = combine2<kMax>(v, dpp<0x140>(v));  // row_mirror
+  v = combine2<kMax>(v, dpp<0x141>(v));  // row_half_mirror
+  v = combine2<kMax>(v, dpp<0xB1>(v));   // xor 1
+  v = combine2<kMax>(v, dpp<0x4E>(v));   // xor 2
+  v = swap_combine16<kMax>(v);           // xor 16
+  if constexpr (MS == 64) v = swap_combine32<kMax>(v);
+  return v;
+}
+
+template <int HD, int MS>
+__global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __restrict__ ws_ml,
+                                                              const float* __restrict__ ws_o, float* __restrict__ out,
+                                                              int n_splits) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const size_t base = static_cast<size_t>(h) * n_splits;
+  // Buffer resources cover exactly this head's n_splits partials: loads past them return 0.
+  const __amdgpu_buffer_rsrc_t ores = make_rsrc(ws_o + base * HD, static_cast<uint32_t>(n_splits) * HD * 4u);
+  const __amdgpu_buffer_rsrc_t mres = make_rsrc(ws_ml + 2 * base, static_cast<uint32_t>(n_splits) * 8u);
+  float ov[MS];
+#pragma unroll
+  for (int j = 0; j < MS; ++j)
+    ov[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ores, (j * HD + d) * 4u, 0, 0));
+  const int js = d & (MS - 1);
+  const float mraw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mres, js * 8u, 0, 0));
+  const float lraw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mres, js * 8u + 4u, 0, 0));
+  const float mj = js < n_splits ? mraw : -INFINITY;
+  const float M = butterfly<MS, true>(mj);
+  const float w = mj == -INFINITY ? 0.0f : expf(mj - M);
+  const float den = butterfly<MS, false>(w * lraw);
+  float num = 0.0f;
+#pragma unroll
+  for (int j = 0; j < MS; ++j)
+    num = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j)), ov[j], num);
+  out[static_cast<size_t>(h) * HD + d] = num / den;
+}
+
+template <int HD, int NK, int G>
+int launch_decode3(const float* q, const uint16_t* kc, const uint16_t* vc, float* ws_ml, float* ws_o, float* out,
+                   int n_splits, int n_kv, int L, const int32_t* start, float scale, hipStream_t st) {
+  hipLaunchKernelGGL((attn_decode_split_kernel<HD, NK, G>), dim3(n_splits, n_kv), dim3(kThreads), 0, st, q, kc, vc,
+                     ws_ml, ws_o, n_kv, L, start, scale);
+  if (n_splits <= 32)
+    hipLaunchKernelGGL((attn_decode_merge_kernel<HD, 32>), dim3(n_kv * G), dim3(HD), 0, st, ws_ml, ws_o, out, n_splits);
+  else
+    hipLaunchKernelGGL((attn_decode_merge_kernel<HD, 64>), dim3(n_kv * G), dim3(HD), 0, st, ws_ml, ws_o, out, n_splits);
+  return launch_status();
+}
+
+template <int HD, int NK>
+int launch_decode2(int g, const float* q, const uint16_t* kc, const uint16_t* vc, float* ws_ml, float* ws_o,
+                   float* out, int n_splits, int n_kv, int L, const int32_t* start, float scale, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_decode3<HD, NK, 1>(q, kc, vc, ws_ml, ws_o, out, n_splits, n_kv, L, start, scale, st);
+    case 2: return launch_decode3<HD, NK, 2>(q, kc, vc, ws_ml, ws_o, out, n_splits, n_kv, L, start, scale, st);
+    case 3: return launch_decode3<HD, NK, 3>(q, kc, vc, ws_ml, ws_o, out, n_splits, n_kv, L, start, scale, st);
+    case 4: return launch_decode3<HD, NK, 4>(q, kc, vc, ws_ml, ws_o, out, n_splits, n_kv, L, start, scale, st);
+    case 8: return launch_decode3<HD, NK, 8>(q, kc, vc, ws_ml, ws_o, out, n_splits, n_kv, L, start, scale, st);
+    default: return Q4_ERR_UNSUPPORTED;
+  }
+}
+
+// The register-resident decode path covers group sizes 1, 2, 3, 4, 8 and at most 64 splits.
+bool decode_fast(int C, int n_q, int n_kv, const AttnPlan& p) {
+  const int g = n_q / n_kv;
+  return C == 1 && p.n_splits <= kDecodeMaxSplits && (g <= 4 || g == 8) && getenv("Q4_ATTN_GENERIC") == nullptr;
+}
+
+int launch_decode(const AttnPlan& p, int hd, int g, const float* q, const uint16_t* kc, const uint16_t* vc,
+                  float* ws_ml, float* ws_o, float* out, int n_kv, int L, const int32_t* start, float scale,
+                  hipStream_t st) {
+  const int n = p.n_splits;
+  if (hd == 128) {  // KPI = 4 keys per wave row: NK = S / 16
+    if (p.S == 32) return launch_decode2<128, 2>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+    if (p.S == 64) return launch_decode2<128, 4>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+    return launch_decode2<128, 8>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+  }
+  // hd == 64: KPI = 8: NK = S / 32
+  if (p.S == 32) return launch_decode2<64, 1>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+  if (p.S == 64) return launch_decode2<64, 2>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+  return launch_decode2<64, 4>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
+}
+
 size_t lds_bytes(int HD, int S) {
   return (static_cast<size_t>(kMaxQ) * HD + static_cast<size_t>(kMaxQ) * S) * 4 + static_cast<size_t>(S) * HD * 2;
 }
@@ -355,6 +651,8 @@ extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_c
   float* ws_ml = static_cast<float*>(workspace);
   float* ws_o = ws_ml + ml_floats(static_cast<size_t>(C) * n_q * p.n_splits);
   const hipStream_t st = as_stream(stream);
+  if (decode_fast(C, n_q, n_kv, p))
+    return launch_decode(p, hd, n_q / n_kv, q, k_cache, v_cache, ws_ml, ws_o, out, n_kv, L, start, scale, st);
   int rc;
   if (hd == 128) {
     if (p.S == 32) rc = launch_split<128, 32>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);

@@ -69,6 +69,29 @@ def test_attn_decode_edges(dev, start, L):
         assert torch.allclose(out.cpu().reshape(8, 128), vc[0].float().repeat_interleave(4, 0), atol=1e-6)
 
 
+@pytest.mark.parametrize("nq,nkv,hd", [(24, 8, 128), (32, 8, 64), (4, 2, 64), (8, 8, 128), (16, 2, 128), (10, 2, 64),
+                                        (16, 8, 64)])
+@pytest.mark.parametrize("L,start", [(32, 7), (256, 200), (1024, 1023), (2048, 1100), (4096, 2049), (8192, 5000),
+                                     (16384, 9000)])
+@pytest.mark.parametrize("path", ["fast", "generic"])
+def test_attn_decode_group_sizes(dev, monkeypatch, nq, nkv, hd, L, start, path):
+    """Decode over group sizes 1-8 (the register-resident kernel takes g in {1, 2, 3, 4, 8} and up to 64
+    splits; g = 5 and L = 16384 take the generic split kernel) and both head dims, each path forced."""
+    if path == "generic":
+        monkeypatch.setenv("Q4_ATTN_GENERIC", "1")
+    else:
+        monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
+    g = torch.Generator().manual_seed(nq * 7 + L + start)
+    q = torch.randn(1, nq, hd, generator=g)
+    kc = torch.randn(L, nkv, hd, generator=g).half()
+    vc = torch.randn(L, nkv, hd, generator=g).half()
+    ref = attn_ref(q, kc, vc, start, L, 1 / math.sqrt(hd))
+    out = ops.attn_bucket(q.to(dev), kc.to(dev), vc.to(dev), L, torch.tensor([start], dtype=torch.int32, device=dev),
+                          1 / math.sqrt(hd))
+    err = (out.cpu().double() - ref).abs().max().item()
+    assert err < 2e-5, (nq, nkv, hd, L, start, path, err)
+
+
 @pytest.mark.parametrize("Cn,start,L,nq,nkv,hd", [(256, 0, 256, 24, 8, 128), (256, 256, 512, 24, 8, 128),
                                                   (16, 0, 64, 4, 2, 64), (8, 13, 32, 8, 2, 32 * 2), (5, 3, 64, 4, 2, 64)])
 def test_attn_prefill_chunk(dev, Cn, start, L, nq, nkv, hd):
