@@ -158,12 +158,27 @@ __device__ __forceinline__ Best block_best(Best b) {
   return r;
 }
 
+// Each thread issues its kArgE coalesced loads (stride 256 inside the block's span) before comparing
+// them, so one pass costs one memory round trip; `better` breaks ties by index, so the visiting
+// order does not matter.
+constexpr int kArgE = 4;
+
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int64_t V,
                                                              Best* __restrict__ ws) {
   Best b{-INFINITY, INT32_MAX};
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < V; i += static_cast<int64_t>(gridDim.x) * 256) {
-    const float v = x[i];
-    if (better(v, static_cast<int32_t>(i), b.v, b.i)) { b.v = v; b.i = static_cast<int32_t>(i); }
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kArgE; base < V;
+       base += static_cast<int64_t>(gridDim.x) * 256 * kArgE) {
+    float v[kArgE];
+#pragma unroll
+    for (int u = 0; u < kArgE; ++u) {
+      const int64_t i = base + u * 256 + threadIdx.x;
+      v[u] = x[i < V ? i : V - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kArgE; ++u) {
+      const int64_t i = base + u * 256 + threadIdx.x;
+      if (i < V && better(v[u], static_cast<int32_t>(i), b.v, b.i)) { b.v = v[u]; b.i = static_cast<int32_t>(i); }
+    }
   }
   const Best r = block_best(b);
   if (threadIdx.x == 0) ws[blockIdx.x] = r;
@@ -178,7 +193,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const Best* __restric
 }
 
 int argmax_blocks(int64_t V) {
-  const int64_t b = (V + 256 * 16 - 1) / (256 * 16);
+  const int64_t b = (V + 256 * kArgE - 1) / (256 * kArgE);
   return static_cast<int>(b < 1 ? 1 : (b > 512 ? 512 : b));
 }
 

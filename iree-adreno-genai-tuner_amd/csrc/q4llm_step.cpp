@@ -142,7 +142,8 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   // Decode (C == 1), when the shapes take the vectorised GEMV (true for every BASELINE model), runs
   // five kernels per layer: qkv GEMV with the input norm in its x staging and RoPE + the K/V cache
   // writes in its epilogue; attention; o-projection + residual; gate/up GEMV with the post-attention
-  // norm and SwiGLU in its epilogue; down-projection + residual. Prefill uses the separate kernels.
+  // norm and SwiGLU in its epilogue; down-projection + residual; after the layers the LM head GEMV
+  // takes the final norm in its x staging. Prefill uses the separate kernels.
   const bool fused = C == 1 && gemv_fusable(D, m->group);
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   for (int i = 0; i < m->n_layers; ++i) {
@@ -171,8 +172,13 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
       Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, lin_ws, lo.lin_bytes, stream));
     }
   }
-  Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
-  Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
+  if (fused) {  // one row: the final norm is the LM head's prologue
+    Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
+                         m->group, stream));
+  } else {
+    Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
+    Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
+  }
   Q4_TRY(argmax_f32(lg, m->vocab, next, amax_ws, lo.amax_bytes, stream));
 #undef Q4_TRY
   return Q4_OK;
