@@ -252,6 +252,8 @@ int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const void* x, i
                 int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg, int grid,
                 void* stream);
 int gemm_f16_num_configs(void);
+/* Number of q4_linear_ws tile entries (Q4_LINEAR_CFG selects one for sweeps and tests). */
+int q4_linear_ws_num_configs(void);
 int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
                     int64_t lda, int64_t ldb, int64_t ldc, int cfg, int split, void* stream);
 

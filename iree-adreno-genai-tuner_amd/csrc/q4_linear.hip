@@ -246,17 +246,28 @@ constexpr size_t kLinLds[] = {LinCfg<128, 128>::kLds, LinCfg<128, 64>::kLds, Lin
 //     (w >> 4i) & 0x000F000F | 0x64006400 make the fp16 pair (1024 + n_i, 1024 + n_{i+4}) and one
 //     packed fp16 add of -1032 gives (n - 8) exactly, in the same (0, 4, 1, 5, ...) order, so the
 //     MFMA's k products pair up with the x planes (the order of k inside one MFMA does not matter);
-//   * x_hi, x_lo and the packed weights stream into an NST-stage LDS ring with direct global -> LDS
-//     16-byte loads (the fp16 GEMM's pipeline; x rows use its conflict-free swizzle), so no VGPRs
-//     stage data and NST-1 K steps are in flight;
+//   * x_hi, x_lo, the packed weights and the step's group scales stream into an NST-stage LDS ring
+//     with direct global -> LDS loads (the fp16 GEMM's pipeline; x rows use its conflict-free
+//     swizzle), so no VGPR is loaded in the loop and NST-1 K steps are in flight; the scales get the
+//     same lookahead as the tiles (loaded into registers one step ahead, they held every step to a
+//     memory round trip: loads complete in issue order);
 //   * per 16-k step two MFMAs (x_hi, x_lo) accumulate a group partial in fp32; at each group end the
-//     partial is scaled by the fp32 group scale (loaded one K step ahead) into the output.
+//     partial is scaled by the fp32 group scale into the output. A wave reads all of its operands of
+//     a stage before its first MFMA, so the LDS latency is paid once per stage;
+//   * with a k split (KS = 2), two waves share each 32x32 output tile and take half of the 16-k steps
+//     of every stage: twice the waves per CU to hide latency at the small M of a prefill chunk; their
+//     sums meet in LDS at the end.
 // ------------------------------------------------------------------------------------------------
 
 constexpr uint32_t kOOBw = 0x80000000u;
 
 __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 16, off, 0, 0, 0);
+}
+
+// 4 bytes per lane from global memory straight into LDS: lane i's dword lands at dst + 4 i.
+__device__ __forceinline__ void load_lds4(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 4, off, 0, 0, 0);
 }
 
 template <int N>
@@ -299,61 +310,43 @@ __device__ __forceinline__ half8 nibbles_to_half8(uint32_t w) {
   return half8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
 }
 
-// Wait until this wave's loads of the stage being consumed have landed: `after` later stages (LPW
-// loads each) and `sc` later scale batches (SPW loads each) may stay in flight. vmcnt needs an
-// immediate, so the (after, sc) pairs are dispatched to constants.
-template <int LPW, int SPW, int A, int S>
-__device__ __forceinline__ void wait_case(int after, int sc) {
-  if (after == A && sc == S) wait_vmcnt<A * LPW + S * SPW>();
-}
-template <int LPW, int SPW, int NST>
-__device__ __forceinline__ void wait_stage(int after, int sc) {
-  wait_case<LPW, SPW, 0, 0>(after, sc);
-  wait_case<LPW, SPW, 0, 1>(after, sc);
-  if constexpr (NST >= 3) {
-    wait_case<LPW, SPW, 0, 2>(after, sc);
-    wait_case<LPW, SPW, 1, 0>(after, sc);
-    wait_case<LPW, SPW, 1, 1>(after, sc);
-    wait_case<LPW, SPW, 1, 2>(after, sc);
-  }
-  if constexpr (NST >= 4) {
-    wait_case<LPW, SPW, 0, 3>(after, sc);
-    wait_case<LPW, SPW, 1, 3>(after, sc);
-    wait_case<LPW, SPW, 2, 0>(after, sc);
-    wait_case<LPW, SPW, 2, 1>(after, sc);
-    wait_case<LPW, SPW, 2, 2>(after, sc);
-    wait_case<LPW, SPW, 2, 3>(after, sc);
-  }
-}
-
-template <int BM, int BN, int WM, int WN, int NST>
+template <int BM, int BN, int WM, int WN, int NST, int KS>
 struct LinWsCfg {
-  static constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
+  static constexpr int kWaves = WM * WN * KS, kThreads = 64 * kWaves;
   static constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   static constexpr int kXRow = 128;                        // bytes per x row per stage (64 fp16)
   static constexpr int kWRow = 32;                         // bytes per weight row per stage (64 nibbles)
-  static constexpr int kStage = 2 * BM * kXRow + BN * kWRow;
+  static constexpr int kSBlk = (BN + 63) / 64;             // 64-column blocks of the scale slots
+  static constexpr int kStage = 2 * BM * kXRow + BN * kWRow + 2 * kSBlk * 256;  // + 2 scale slots
   static constexpr int kAI = BM / 8 / kWaves;             // x direct loads per wave, per plane
   static constexpr int kBI = (BN / 32 + kWaves - 1) / kWaves;  // weight direct loads per wave (32 rows each)
-  static constexpr int kLPW = 2 * kAI + kBI;
-  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + 1024;  // + junk for spare weight loads
+  static constexpr int kSI = (2 * kSBlk + kWaves - 1) / kWaves;  // scale direct loads per wave
+  static constexpr int kLPW = 2 * kAI + kBI + kSI;
+  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + 1024;  // + junk for spare loads
   static_assert(TM >= 1 && TN >= 1 && kAI * 8 * kWaves == BM, "tile shape");
-  static constexpr int kSPW = 2 * TN;                      // scale loads per wave per K step
-  static_assert(NST >= 2 && NST <= 4 && kLPW * (NST - 2) + kSPW * (NST - 1) < 64, "stages");
+  static_assert(NST >= 2 && NST <= 8 && kLPW * (NST - 1) < 64, "stages: vmcnt holds at most 63");
+  static_assert(KS == 1 || KS == 2 || KS == 4, "k split over 1, 2 or 4 wave groups");
+  static constexpr size_t kRed = static_cast<size_t>(KS - 1) * WM * WN * TM * TN * 16 * 64 * 4;
+  static_assert(kRed <= static_cast<size_t>(NST) * kStage, "k-split reduction fits in the stages");
 };
 
-template <int BM, int BN, int WM, int WN, int NST>
-__global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
+template <int BM, int BN, int WM, int WN, int NST, int KS>
+__global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
     const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n) {
-  using G = LinWsCfg<BM, BN, WM, WN, NST>;
+  using G = LinWsCfg<BM, BN, WM, WN, NST, KS>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int spr = K / group;
+  const int gshift = __builtin_ctz(group);  // the host passes power-of-two groups only
+  const int spr = K >> gshift;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  // wave -> (k group ks, tile row wm, tile column wn): the KS wave groups share the tile and each
+  // takes 4 / KS of the four 16-k steps of every 64-k stage; their sums meet in LDS at the end.
+  const int ks = wave / (WM * WN), wt = wave - ks * (WM * WN);
+  const int wm = wt / WN, wn = wt % WN;
+  constexpr int KK = 4 / KS;
   const uint32_t xbytes = static_cast<uint32_t>(M) * K * 2u;
   const __amdgpu_buffer_rsrc_t hr = make_rsrc(XH, xbytes);
   const __amdgpu_buffer_rsrc_t lr = make_rsrc(XL, xbytes);
@@ -401,27 +394,33 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
     for (int j = 0; j < G::kBI; ++j)
       load_lds16(wr, wreal[j] ? sw + (wave + j * G::kWaves) * 1024 : junk,
                  kin && woff[j] != kOOBw ? woff[j] + k0 / 2 : kOOBw);
+    // Scales: instruction i = wave + j * kWaves (< 2 kSBlk) fills slot i / kSBlk (the step's first or
+    // last group; a 64-k step touches at most two groups of >= 32) for the 64 columns of block
+    // i % kSBlk: lane -> column, the aligned dword holding its fp16 scale (the buffer range is rounded
+    // up to 4 bytes; device allocations are 256-byte granular). Spare instructions fill the junk area.
+    unsigned char* ss = sw + BN * G::kWRow;
+    const int g0 = k0 >> gshift, g1 = (k0 + 63) >> gshift;
+#pragma unroll
+    for (int j = 0; j < G::kSI; ++j) {
+      const int i = wave + j * G::kWaves;
+      const bool real = i < 2 * G::kSBlk;
+      const int slot = i / G::kSBlk, blk = i - slot * G::kSBlk;
+      const int col = n0 + blk * 64 + lane;
+      const uint32_t e = static_cast<uint32_t>(col) * spr + (slot ? g1 : g0);
+      load_lds4(sr, real ? ss + (slot * G::kSBlk + blk) * 256 : junk,
+                real && kin && col < N ? (e >> 1) * 4u : kOOBw);
+    }
   };
 
-  // Scales of the groups in K step kt for this lane's TN columns (2 slots: a 64-k step touches at
-  // most two groups of >= 32), loaded one K step ahead as the aligned dword holding the fp16 value
-  // (the buffer range is rounded up to 4 bytes; device allocations are 256-byte granular). No
-  // conditions: a column past N lies past the end of the scales (the range check returns zeros),
-  // and the prefetch past the last step reads an unused in-range value or zeros.
   auto scale_elem = [&](int j, int g) -> uint32_t {
     const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
     return static_cast<uint32_t>(col) * spr + g;
   };
-  auto scale_load = [&](int kt, uint32_t (&s)[2][G::TN]) {
-    const int g0 = (kt * 64) / group, g1 = (kt * 64 + 63) / group;
-#pragma unroll
-    for (int j = 0; j < G::TN; ++j) {
-      s[0][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(sr, (scale_elem(j, g0) >> 1) * 4u, 0, 0));
-      s[1][j] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(sr, (scale_elem(j, g1) >> 1) * 4u, 0, 0));
-    }
-  };
-  auto scale_of = [&](const uint32_t (&s)[2][G::TN], int slot, int j, int g) {
-    return half_bits_to_float(static_cast<uint16_t>(s[slot][j] >> (16 * (scale_elem(j, g) & 1))));
+  // scale of group g for this lane's column in tile column j, from slot `slot` of the stage at ss
+  auto scale_of = [&](const unsigned char* ss, int slot, int j, int g) {
+    const int cl = wn * G::WTN + j * 32 + (lane & 31);
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(ss + slot * G::kSBlk * 256 + cl * 4);
+    return half_bits_to_float(static_cast<uint16_t>(v >> (16 * (scale_elem(j, g) & 1))));
   };
 
   float16v acc[G::TM][G::TN], part[G::TM][G::TN];
@@ -435,51 +434,64 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
   const int arow = wm * G::WTM + (lane & 31);
   const int brow = wn * G::WTN + (lane & 31);
   const int nk = K / 64;
-  // Load order per wave: scales of step 0, stages 0..NST-2, then per step kt: the scales of step
-  // kt+1 and stage kt+NST-1. At step kt the loads issued after stage kt are NST-2 stages and
-  // min(kt, NST-2) scale batches (the compiler barriers keep this order). The scale registers
-  // alternate between two sets (the loop is unrolled by two), so no copy waits on a fresh load,
-  // and the newest loads in flight are always stage loads.
-  auto step = [&](int kt, const uint32_t (&scur)[2][G::TN], uint32_t (&snext)[2][G::TN]) {
-    wait_stage<G::kLPW, G::kSPW, NST>(NST - 2, min(kt, NST - 2));
+  // Every load of a step (x planes, weights, scales) goes straight to LDS; when at most NST-2 steps'
+  // loads of this wave are in flight, its part of step kt has landed, and the barrier publishes the
+  // whole stage. No VGPR is loaded in the loop, so the compiler adds no waits of its own.
+  auto step = [&](int kt) {
+    wait_vmcnt<(NST - 2) * G::kLPW>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    scale_load(kt + 1, snext);  // past the last step: unused
     asm volatile("" ::: "memory");
     issue(kt + NST - 1, (kt + NST - 1) % NST);
     asm volatile("" ::: "memory");
     const unsigned char* sh = lds + (kt % NST) * G::kStage;
     const unsigned char* sl = sh + BM * G::kXRow;
     const unsigned char* sw = sl + BM * G::kXRow;
+    const unsigned char* ss = sw + BN * G::kWRow;
     const int k0 = kt * 64;
+    // All operand reads of the step first (x_hi, x_lo and the nibble words of the 4 16-k steps), so the
+    // LDS latency is paid once per step instead of once per 16-k step.
+    half8 fh[KK][G::TM], fl[KK][G::TM];
+    uint32_t fw[KK][G::TN];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = 2 * kk + (lane >> 5);  // this lane's 8-k chunk of the step
+    for (int q = 0; q < KK; ++q) {
+      const int kk = ks * KK + q;
+      const int c = 2 * kk + (lane >> 5);  // this lane's 8-k chunk of the 16-k step
       const int xs = (c ^ ((lane >> 1) & 7)) << 4;
-      half8 fh[G::TM], fl[G::TM], fb[G::TN];
 #pragma unroll
       for (int i = 0; i < G::TM; ++i) {
-        fh[i] = *reinterpret_cast<const half8*>(sh + (arow + 32 * i) * G::kXRow + xs);
-        fl[i] = *reinterpret_cast<const half8*>(sl + (arow + 32 * i) * G::kXRow + xs);
+        fh[q][i] = *reinterpret_cast<const half8*>(sh + (arow + 32 * i) * G::kXRow + xs);
+        fl[q][i] = *reinterpret_cast<const half8*>(sl + (arow + 32 * i) * G::kXRow + xs);
       }
 #pragma unroll
-      for (int j = 0; j < G::TN; ++j)
-        fb[j] = nibbles_to_half8(*reinterpret_cast<const uint32_t*>(sw + (brow + 32 * j) * G::kWRow + 4 * c));
+      for (int j = 0; j < G::TN; ++j) fw[q][j] = *reinterpret_cast<const uint32_t*>(sw + (brow + 32 * j) * G::kWRow + 4 * c);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs that use them
+#pragma unroll
+    for (int q = 0; q < KK; ++q) {
+      const int kk = ks * KK + q;
+      half8 fb[G::TN];
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) fb[j] = nibbles_to_half8(fw[q][j]);
 #pragma unroll
       for (int i = 0; i < G::TM; ++i)
 #pragma unroll
         for (int j = 0; j < G::TN; ++j) {
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[i], fb[j], part[i][j], 0, 0, 0);
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[i], fb[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[q][i], fb[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[q][i], fb[j], part[i][j], 0, 0, 0);
         }
       const int k = k0 + 16 * kk;
-      if ((k + 16) % group == 0) {  // the group ends with this 16-k step: apply its scale
-        const int g = k / group;
-        const int gi = g - k0 / group;
+      // Apply the group's scale when the group ends with this 16-k step, or (k split) when this is the
+      // wave's last 16-k step of the stage and its group ends inside the stage (another wave group
+      // holds the rest of it).
+      const bool ends_here = ((k + 16) & (group - 1)) == 0;
+      const bool ends_in_stage = KS > 1 && q == KK - 1 && ((((k >> gshift) + 1) << gshift) <= k0 + 64);
+      if (ends_here || ends_in_stage) {
+        const int g = k >> gshift;
+        const int gi = g - (k0 >> gshift);
 #pragma unroll
         for (int j = 0; j < G::TN; ++j) {
-          const float sc = scale_of(scur, gi, j, g);
+          const float sc = scale_of(ss, gi, j, g);
 #pragma unroll
           for (int i = 0; i < G::TM; ++i)
 #pragma unroll
@@ -491,14 +503,38 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
       }
     }
   };
-  uint32_t sa[2][G::TN], sb[2][G::TN];
-  scale_load(0, sa);
-  asm volatile("" ::: "memory");
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s) issue(s, s);
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(kt, sa, sb);
-    if (kt + 1 < nk) step(kt + 1, sb, sa);
+  for (int kt = 0; kt < nk; ++kt) step(kt);
+
+  if constexpr (KS > 1) {
+    // k-split: wave groups 1..KS-1 hand their sums to group 0 through LDS (the stage memory; the
+    // out-of-range loads of the last steps must land before it is reused). Layout [group][wave][tile]
+    // [e][lane]: every access is one 256-byte row.
+    wait_vmcnt<0>();
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);
+    auto slot = [&](int g2, int i, int j, int e) {
+      return red + ((((g2 * (WM * WN) + wt) * G::TM + i) * G::TN + j) * 16 + e) * 64 + lane;
+    };
+    if (ks > 0) {
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) *slot(ks - 1, i, j, e) = acc[i][j][e];
+    }
+    __syncthreads();  // waits for this wave's LDS writes (lgkmcnt) before the barrier
+    if (ks > 0) return;
+#pragma unroll
+    for (int g2 = 0; g2 < KS - 1; ++g2)
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += *slot(g2, i, j, e);
   }
 
 #pragma unroll
@@ -517,29 +553,33 @@ __global__ __launch_bounds__(64 * WM * WN) void q4_linear_ws_kernel(
 }
 
 struct LinWsTile {
-  int bm, bn, wm, wn, nst;
+  int bm, bn, wm, wn, nst, ks;
 };
 // Explicit tile list (index stable for Q4_LINEAR_CFG sweeps).
 constexpr LinWsTile kLinWsTiles[] = {
-    {128, 128, 2, 2, 4},  // 0: 4 waves of 64x64, 4 stages (144 KB)
-    {64, 128, 2, 2, 4},   // 1: 4 waves of 32x64, 4 stages (80 KB)
-    {64, 64, 2, 2, 4},    // 2: 4 waves of 32x32, 4 stages (72 KB)
-    {128, 64, 2, 2, 4},   // 3: 4 waves of 64x32 (104 KB)
+    {64, 64, 2, 2, 4, 1},    // 0: 4 waves of 32x32, 4 stages (77 KB)
+    {32, 64, 1, 2, 4, 2},    // 1: 4 waves: 2 tiles of 32x32, each k-split over 2 waves (52 KB)
+    {64, 64, 2, 2, 4, 2},    // 2: 8 waves: 4 tiles of 32x32, k-split over 2
+    {128, 64, 2, 2, 4, 2},   // 3: 8 waves: 4 tiles of 64x32, k-split over 2
+    {32, 32, 1, 1, 4, 2},    // 4: 2 waves: one 32x32 tile, k-split over 2
+    {128, 128, 2, 2, 4, 1},  // 5: 4 waves of 64x64 (152 KB)
 };
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
                          int, int, int, int);
 template <int I>
 constexpr LinWsFn lin_ws_fn() {
   constexpr LinWsTile t = kLinWsTiles[I];
-  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst>;
+  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>;
 }
 template <int I>
 constexpr size_t lin_ws_lds() {
   constexpr LinWsTile t = kLinWsTiles[I];
-  return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst>::kLds;
+  return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
 }
-constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(), lin_ws_fn<3>()};
-constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(), lin_ws_lds<3>()};
+constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(),
+                                 lin_ws_fn<3>(), lin_ws_fn<4>(), lin_ws_fn<5>()};
+constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(),
+                                lin_ws_lds<3>(), lin_ws_lds<4>(), lin_ws_lds<5>()};
 constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
 
 }  // namespace
@@ -566,10 +606,15 @@ int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_
   return launch_status();
 }
 
-// Fixed rule: the largest tile (in list order 0, 3, 1, 2) giving at least 256 workgroups, else the
-// smallest. Q4_LINEAR_CFG overrides for sweeps.
+int q4_linear_ws_num_tiles() { return kNumLinWs; }
+
+// Fixed rule from a sweep of every entry over the 3B prefill shapes at M = 128, 256 and 1024 (graph
+// replays on one MI355X): the 32x64 k-split tile while it gives at most 768 workgroups (every
+// M <= 256 chunk of the 3072-, 5120- and 8192-wide projections), else 64x64. Q4_LINEAR_CFG overrides.
 int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
                         int64_t N, int64_t K, int group, void* ws, hipStream_t st) {
+  // the pipelined kernel indexes groups by shifts: other group sizes take the workspace-free kernel
+  if (group & (group - 1)) return q4_linear_launch(x, M, qw, sc, y, res, N, K, group, -1, st);
   uint16_t* xh = static_cast<uint16_t*>(ws);
   uint16_t* xl = xh + M * K;
   const int64_t chunks = M * K / 8;
@@ -579,16 +624,7 @@ int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
-  if (ti < 0) {
-    ti = 2;
-    for (int i : {0, 3, 1, 2}) {
-      const LinWsTile& t = kLinWsTiles[i];
-      if (((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) >= 256) {
-        ti = i;
-        break;
-      }
-    }
-  }
+  if (ti < 0) ti = ((M + 31) / 32) * ((N + 63) / 64) <= 768 ? 1 : 0;
   const LinWsTile& t = kLinWsTiles[ti];
   const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
   const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
@@ -596,7 +632,7 @@ int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint
     Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kLinWsFns[ti]),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[ti])));
   }
-  hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
+  hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
                      (int)M, (int)N, (int)K, group, tiles_n);
   return launch_status();
 }
@@ -615,6 +651,8 @@ int linear_args(const float* x, int64_t M, const int32_t* qweight, const uint16_
   return Q4_OK;
 }
 }  // namespace
+
+extern "C" int q4_linear_ws_num_configs(void) { return q4::q4_linear_ws_num_tiles(); }
 
 extern "C" int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes) {
   if (!bytes) return Q4_ERR_NULL;

@@ -41,6 +41,7 @@ SIGNATURES = {
     "gemm_f16_nt": [p, p, p, i64, i64, i64, i64, i64, i64, p],
     "gemm_f16_nt_cfg": [p, p, p, i64, i64, i64, i64, i64, i64, i32, i32, p],
     "gemm_f16_num_configs": [],
+    "q4_linear_ws_num_configs": [],
     "attn_workspace_bytes": [i32, i32, i32, i32, i32, C.POINTER(sz)],
     "attn_bucket": [p, i32, p, p, p, i32, i32, i32, i32, i32, p, f32, p, sz, p],
     "rmsnorm_f32": [p, p, p, i64, i64, f32, p, p],

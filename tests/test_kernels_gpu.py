@@ -179,10 +179,11 @@ def test_q4_linear_fp32_accuracy(dev, M, N, K, group):
 
 @pytest.mark.parametrize("M,N,K,group", [(256, 5120, 3072, 128), (256, 3072, 8192, 128), (16, 1408, 256, 32),
                                          (16, 256, 704, 32), (7, 100, 128, 64), (300, 3072, 3072, 128),
-                                         (256, 16384, 3072, 128), (33, 200, 320, 64)])
+                                         (256, 16384, 3072, 128), (33, 200, 320, 64), (20, 130, 192, 96)])
 def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch):
     """The workspace entry point (x split into fp16 hi/lo planes, multi-stage pipeline) keeps the
-    fp32-level accuracy of q4_linear on every tile of its list, with ragged M and N."""
+    fp32-level accuracy of q4_linear on every tile of its list, with ragged M and N; a group that is not
+    a power of two (96) takes the workspace-free kernel."""
     g = torch.Generator().manual_seed(M + N + K)
     w = torch.randn(N, K, generator=g) * 0.02
     x = torch.randn(M, K, generator=g)
@@ -191,7 +192,8 @@ def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch)
     ref = x.double() @ R.dequantize_q4(qw, sc, group).double().T
     rms = ref.pow(2).mean().sqrt().item()
     xd, qd, sd = x.to(dev), qw.to(dev), sc.to(dev)
-    for cfg in ("", "0", "1", "2", "3"):
+    from q4llm._lib import LIB
+    for cfg in [""] + [str(i) for i in range(LIB.raw("q4_linear_ws_num_configs")())]:
         monkeypatch.setenv("Q4_LINEAR_CFG", cfg)
         y = nan_like((M, N), torch.float32, dev)
         ops.q4_linear_ws(xd, qd, sd, group, out=y)
