@@ -97,15 +97,27 @@ __device__ __forceinline__ float dot_chunk_f32(const uint4& w, const float4* __r
 
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
-__device__ __forceinline__ float dot_chunk_f16(const uint4& w, const uint4* __restrict__ xs, int cpr, int c) {
-  // xs slot j (one uint4 per word): half2 pairs (x0,x4), (x1,x5), (x2,x6), (x3,x7)
+// x slots of one chunk for dot_chunk_f16: xs slot j (one uint4 per word) holds the half2 pairs
+// (x0,x4), (x1,x5), (x2,x6), (x3,x7)
+struct XChunkF16 {
+  uint4 p[4];
+};
+
+__device__ __forceinline__ XChunkF16 x_chunk_f16(const uint4* __restrict__ xs, int cpr, int c) {
+  XChunkF16 x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x.p[j] = xs[j * cpr + c];
+  return x;
+}
+
+__device__ __forceinline__ float dot_chunk_f16(const uint4& w, const XChunkF16& x) {
   float t = 0.0f;
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t v = words[j];
     const uint32_t v8 = v >> 8;
-    const uint4 xp = xs[j * cpr + c];
+    const uint4 xp = x.p[j];
     // (1024 + n0, 1024 + n4), (64 + n1, 64 + n5), (1024 + n2, 1024 + n6), (64 + n3, 64 + n7)
     const uint32_t m0 = (v & 0x000F000Fu) | 0x64006400u;
     const uint32_t m1 = (v & 0x00F000F0u) | 0x54005400u;
@@ -371,18 +383,40 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
   // Accumulate one item; on the last K pass reduce over the LPR lanes and store.
   auto compute_item = [&](int it, const Item<LPR, CPL, R>& d) {
     const int kp = it % n_kpass;
+    // out-of-range slots carry zero weights and a zero scale; clamp only the LDS address
+    auto chunk = [&](int i) { return min(kp * (LPR * CPL) + i * LPR + lr, cpr - 1); };
+    // fp16 x with up to 6 waves (measured: 5120x3072 3.86 -> 3.76 us, 3072x8192 4.94 -> 4.88 us; the
+    // 8-wave 16384x3072 entry lost 0.5-1 us, so it keeps reading x per chunk): every x slot and
+    // correction of the item is read from LDS before the first weight is used, so the chunks that land
+    // last carry only their own arithmetic
+    if constexpr (kF16X && WAVES <= 6) {
+      XChunkF16 xc[CPL];
+      float cc[CPL];
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      // out-of-range slots carry zero weights and a zero scale; clamp only the LDS address
-      const int c = min(kp * (LPR * CPL) + i * LPR + lr, cpr - 1);
-      const float4 cw = reinterpret_cast<const float4*>(corr_w)[c];
-      const float cc = (cw.x + cw.y) + (cw.z + cw.w);
+      for (int i = 0; i < CPL; ++i) {
+        xc[i] = x_chunk_f16(xs, cpr, chunk(i));
+        const float4 cw = reinterpret_cast<const float4*>(corr_w)[chunk(i)];
+        cc[i] = (cw.x + cw.y) + (cw.z + cw.w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float t;
-        if constexpr (kF16X) t = dot_chunk_f16(d.w[r][i], xs, cpr, c);
-        else t = dot_chunk_f32(d.w[r][i], reinterpret_cast<const float4*>(xs), cpr, c);
-        acc[r] = fmaf(half_bits_to_float(d.s[r][i]), t - cc, acc[r]);
+      for (int i = 0; i < CPL; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[r] = fmaf(half_bits_to_float(d.s[r][i]), dot_chunk_f16(d.w[r][i], xc[i]) - cc[i], acc[r]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = chunk(i);
+        const float4 cw = reinterpret_cast<const float4*>(corr_w)[c];
+        const float cc = (cw.x + cw.y) + (cw.z + cw.w);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float t;
+          if constexpr (kF16X) t = dot_chunk_f16(d.w[r][i], x_chunk_f16(xs, cpr, c));
+          else t = dot_chunk_f32(d.w[r][i], reinterpret_cast<const float4*>(xs), cpr, c);
+          acc[r] = fmaf(half_bits_to_float(d.s[r][i]), t - cc, acc[r]);
+        }
       }
     }
     if (kp == n_kpass - 1) {
