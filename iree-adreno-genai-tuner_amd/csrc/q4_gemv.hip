@@ -73,16 +73,27 @@ inline size_t lds_bytes(int64_t K) {
   return static_cast<size_t>(cpr) * (XLayout<kF16X>::kSlots * 16 + 16) + XLayout<kF16X>::kSlots * 16 + 16;
 }
 
-__device__ __forceinline__ float dot_chunk_f32(const uint4& w, const float4* __restrict__ xs, int cpr, int c) {
-  // xs slot layout per word j (2 float4): {x0,x2,x4,x6}, {x1,x3,x5,x7}
+// x slots of one chunk for dot_chunk_f32: per word j two float4, {x0,x2,x4,x6} and {x1,x3,x5,x7}
+struct XChunkF32 {
+  float4 p[8];
+};
+
+__device__ __forceinline__ XChunkF32 x_chunk_f32(const float4* __restrict__ xs, int cpr, int c) {
+  XChunkF32 x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x.p[j] = xs[j * cpr + c];
+  return x;
+}
+
+__device__ __forceinline__ float dot_chunk_f32(const uint4& w, const XChunkF32& x) {
   float t = 0.0f;
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t lo = words[j] & 0x0F0F0F0Fu;
     const uint32_t hi = (words[j] >> 4) & 0x0F0F0F0Fu;
-    const float4 xe = xs[(2 * j) * cpr + c];
-    const float4 xo = xs[(2 * j + 1) * cpr + c];
+    const float4 xe = x.p[2 * j];
+    const float4 xo = x.p[2 * j + 1];
     t = fmaf(xe.x, static_cast<float>(lo & 0xFFu), t);
     t = fmaf(xe.y, static_cast<float>((lo >> 8) & 0xFFu), t);
     t = fmaf(xe.z, static_cast<float>((lo >> 16) & 0xFFu), t);
@@ -404,6 +415,22 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r)
           acc[r] = fmaf(half_bits_to_float(d.s[r][i]), dot_chunk_f16(d.w[r][i], xc[i]) - cc[i], acc[r]);
+    } else if constexpr (!kF16X && CPL <= 3) {
+      // fp32 x, the same order (3072x3072 o-projection: 3.62 -> 3.36 us, 5120x3072 4.73 -> 4.34 us)
+      XChunkF32 xc[CPL];
+      float cc[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        xc[i] = x_chunk_f32(reinterpret_cast<const float4*>(xs), cpr, chunk(i));
+        const float4 cw = reinterpret_cast<const float4*>(corr_w)[chunk(i)];
+        cc[i] = (cw.x + cw.y) + (cw.z + cw.w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < CPL; ++i)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[r] = fmaf(half_bits_to_float(d.s[r][i]), dot_chunk_f32(d.w[r][i], xc[i]) - cc[i], acc[r]);
     } else {
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
@@ -414,7 +441,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4_gemv_kernel(
         for (int r = 0; r < R; ++r) {
           float t;
           if constexpr (kF16X) t = dot_chunk_f16(d.w[r][i], x_chunk_f16(xs, cpr, c));
-          else t = dot_chunk_f32(d.w[r][i], reinterpret_cast<const float4*>(xs), cpr, c);
+          else t = dot_chunk_f32(d.w[r][i], x_chunk_f32(reinterpret_cast<const float4*>(xs), cpr, c));
           acc[r] = fmaf(half_bits_to_float(d.s[r][i]), t - cc, acc[r]);
         }
       }
