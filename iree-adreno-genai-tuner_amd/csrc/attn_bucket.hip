@@ -15,6 +15,7 @@
 // reads only the valid prefix of the bucket). `start` is read on the device.
 #include "q4_common.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -30,16 +31,24 @@ struct AttnPlan {
   int CB;        // query rows per workgroup
   int n_splits;  // ceil(L / S)
   int n_cblk;    // ceil(C / CB)
+  bool mfma;     // prefill chunk on the matrix cores (attn_prefill_mfma_kernel)
 };
+
+constexpr int kMfmaMaxG = 8;  // query heads per KV head (one wave each) of the matrix-core prefill
 
 AttnPlan plan_for(int C, int n_q, int n_kv, int L) {
   const int g = n_q / n_kv;
   AttnPlan p;
+  p.mfma = false;
   if (C == 1) {
     p.CB = 1;
     p.S = L <= 1024 ? 32 : (L <= 2048 ? 64 : 128);
     const char* ov = getenv("Q4_ATTN_S");  // sweep override: keys per split (32, 64 or 128)
     if (ov && (atoi(ov) == 32 || atoi(ov) == 64 || atoi(ov) == 128)) p.S = atoi(ov);
+  } else if (g <= kMfmaMaxG && getenv("Q4_ATTN_GENERIC") == nullptr) {
+    p.mfma = true;
+    p.CB = 32;
+    p.S = L <= 256 ? 64 : 128;
   } else {
     p.CB = kMaxQ / g < C ? kMaxQ / g : C;
     p.S = 64;
@@ -591,6 +600,198 @@ int launch_decode(const AttnPlan& p, int hd, int g, const float* q, const uint16
   return launch_decode2<64, 4>(g, q, kc, vc, ws_ml, ws_o, out, n, n_kv, L, start, scale, st);
 }
 
+// ---- Prefill (C > 1): flash attention on the fp16 matrix cores ----------------------------------
+//
+// Workgroup (key split, KV head, block of 32 query rows) with one wave per query head of the group.
+// Per 32-key block: S^T = K Q^T (v_mfma_f32_32x32x16_f16, K from LDS as the A operand, the fp32
+// queries split into fp16 hi + lo as two B operands, so the products keep fp32-level accuracy), the
+// mask (key <= pos, key < L) and an online softmax per query (a lane holds one query column; the
+// other half of its keys sits in lane ^ 32), then O^T += V^T P^T with P split into fp16 hi + lo the
+// same way. The S^T accumulator is used directly as the P^T operand: its keys are fed in a fixed
+// permutation (lane half h supplies keys 16u + 8(i/4) + 4h + i%4) and V^T is read from LDS in the
+// same order, so no transpose of P is needed. O^T's column is the lane's query, so the softmax
+// rescale is per lane. The partial (m, l, o) of each (row, head, split) goes to the workspace and
+// attn_combine_kernel merges the splits. The next key block's K/V rows are loaded into registers
+// while the current block is computed; the workgroup has at least 4 waves for that staging (waves
+// past the group size only stage).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+template <int HD>
+__device__ __forceinline__ int kswz(int r) {  // 16-byte chunk swizzle of a key row in LDS
+  return HD == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * kMfmaMaxG) void attn_prefill_mfma_kernel(
+    const float* __restrict__ q, int q_stride, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    float* __restrict__ ws_ml, float* __restrict__ ws_o, int C, int n_q, int n_kv, int L, int S,
+    const int32_t* __restrict__ start_p, float scale) {
+  constexpr int KSTEPS = HD / 16;       // 16-dim k-steps of the score MFMAs
+  constexpr int OT = HD / 32;           // 32-dim output tiles
+  constexpr int KCH = HD / 8;           // 16-byte chunks per key row
+  constexpr int VT_PITCH = 32 * 2 + 8;  // bytes per V^T row: 32 keys + 8 bytes (conflict-free 8-byte reads)
+  constexpr int kMaxCh = 32 * KCH / 256; // staging chunks per thread (at least 4 waves)
+  __shared__ __attribute__((aligned(16))) unsigned char Ks[32 * HD * 2];
+  __shared__ __attribute__((aligned(16))) unsigned char Vt[HD * VT_PITCH];
+  const int g = n_q / n_kv;
+  const int split = blockIdx.x, hk = blockIdx.y, qb = blockIdx.z;
+  const int n_splits = gridDim.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool computes = wave < g;       // waves past the group size only stage K and V
+  const int h = hk * g + (computes ? wave : 0);
+  const int half = lane >> 5, ql = lane & 31;
+  const int nthr = blockDim.x;
+  const int c0 = qb * 32;
+  const int start = start_p[0];
+  const int pos_max = start + min(c0 + 31, C - 1);
+  const int k0 = split * S;
+  const int k_end = min(min(k0 + S, L), pos_max + 1);
+  if (k0 >= k_end) return;  // no row of the block sees a key of this split: the merge never reads it
+  const int c = c0 + ql;
+  const bool row_ok = computes && c < C;
+  const int pos = start + c;
+
+  // Q^T operand (column = this lane's query, k = dims 16 t + 8 half + i), split into fp16 hi + lo
+  half8 qh[KSTEPS], qlo[KSTEPS];
+#pragma unroll
+  for (int t = 0; t < KSTEPS; ++t) {
+    float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (row_ok) {
+      const float4* qp = reinterpret_cast<const float4*>(q + static_cast<size_t>(c) * q_stride +
+                                                         static_cast<size_t>(h) * HD + 16 * t + 8 * half);
+      const float4 a = qp[0], b = qp[1];
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const _Float16 hi = static_cast<_Float16>(f[i]);
+      qh[t][i] = hi;
+      qlo[t][i] = static_cast<_Float16>(f[i] - static_cast<float>(hi));
+    }
+  }
+
+  const uint32_t cache_bytes = static_cast<uint32_t>(L) * n_kv * HD * 2u;
+  const __amdgpu_buffer_rsrc_t kres = make_rsrc(kc, cache_bytes);
+  const __amdgpu_buffer_rsrc_t vres = make_rsrc(vc, cache_bytes);
+  // K/V rows of a 32-key block: chunk ch = threadIdx.x + i * nthr (row ch / KCH, 16-byte chunk ch % KCH);
+  // keys past L read out of range (zeros).
+  uint4 kpre[kMaxCh], vpre[kMaxCh];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < kMaxCh; ++i) {
+      const int ch = threadIdx.x + i * nthr;
+      const int r = ch / KCH, cc = ch - (ch / KCH) * KCH;
+      const uint32_t off = ch < 32 * KCH ? (static_cast<uint32_t>(kb + r) * n_kv + hk) * (HD * 2u) + cc * 16u
+                                         : 0x80000000u;
+      kpre[i] = buf_load16(kres, off);
+      vpre[i] = buf_load16(vres, off);
+    }
+  };
+  auto stage_block = [&]() {
+#pragma unroll
+    for (int i = 0; i < kMaxCh; ++i) {
+      const int ch = threadIdx.x + i * nthr;
+      if (ch < 32 * KCH) {
+        const int r = ch / KCH, cc = ch - (ch / KCH) * KCH;
+        *reinterpret_cast<uint4*>(Ks + r * (HD * 2) + ((cc ^ kswz<HD>(r)) << 4)) = kpre[i];
+        const uint32_t w[4] = {vpre[i].x, vpre[i].y, vpre[i].z, vpre[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<uint16_t*>(Vt + (cc * 8 + j) * VT_PITCH + r * 2) =
+              static_cast<uint16_t>(w[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+  };
+
+  float16v o[OT];
+#pragma unroll
+  for (int tt = 0; tt < OT; ++tt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[tt][e] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+
+  load_block(k0);
+  for (int kb = k0; kb < k_end; kb += 32) {
+    stage_block();
+    __syncthreads();
+    if (kb + 32 < k_end) load_block(kb + 32);  // in flight during this block's MFMAs
+
+    // S^T = K Q^T: 32 keys (rows) x 32 queries (columns)
+    float16v sacc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sacc[e] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < KSTEPS; ++t) {
+      const half8 ka = *reinterpret_cast<const half8*>(Ks + ql * (HD * 2) + (((2 * t + half) ^ kswz<HD>(ql)) << 4));
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[t], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qlo[t], sacc, 0, 0, 0);
+    }
+    float sv[16];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = kb + 8 * (e >> 2) + 4 * half + (e & 3);
+      const bool ok = row_ok && key <= pos && key < L;
+      sv[e] = ok ? sacc[e] * scale : -INFINITY;
+      mb = fmaxf(mb, sv[e]);
+    }
+    mb = swap_combine32<true>(mb);
+    const float m_new = fmaxf(m, mb);
+    const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+    float ls = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sv[e] = sv[e] == -INFINITY ? 0.0f : expf(sv[e] - m_new);
+      ls += sv[e];
+    }
+    ls = swap_combine32<false>(ls);
+    l = l * alpha + ls;
+    m = m_new;
+#pragma unroll
+    for (int tt = 0; tt < OT; ++tt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[tt][e] *= alpha;
+
+    // O^T += V^T P^T over two 16-key steps
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      half8 ph, pl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const _Float16 hi = static_cast<_Float16>(sv[8 * u + i]);
+        ph[i] = hi;
+        pl[i] = static_cast<_Float16>(sv[8 * u + i] - static_cast<float>(hi));
+      }
+#pragma unroll
+      for (int tt = 0; tt < OT; ++tt) {
+        const unsigned char* vrow = Vt + (32 * tt + ql) * VT_PITCH;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + (16 * u + 4 * half) * 2);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + (16 * u + 8 + 4 * half) * 2);
+        const uint4 vv = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        const half8 va = __builtin_bit_cast(half8, vv);
+        o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph, o[tt], 0, 0, 0);
+        o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl, o[tt], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave is done with this block's K and V^T
+  }
+
+  if (row_ok) {
+    const size_t idx = (static_cast<size_t>(c) * n_q + h) * n_splits + split;
+    if (half == 0) {
+      ws_ml[2 * idx] = m;
+      ws_ml[2 * idx + 1] = l;
+    }
+#pragma unroll
+    for (int tt = 0; tt < OT; ++tt)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        reinterpret_cast<float4*>(ws_o + idx * HD + 32 * tt + 8 * a + 4 * half)[0] =
+            make_float4(o[tt][4 * a], o[tt][4 * a + 1], o[tt][4 * a + 2], o[tt][4 * a + 3]);
+  }
+}
+
 size_t lds_bytes(int HD, int S) {
   return (static_cast<size_t>(kMaxQ) * HD + static_cast<size_t>(kMaxQ) * S) * 4 + static_cast<size_t>(S) * HD * 2;
 }
@@ -653,8 +854,17 @@ extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_c
   const hipStream_t st = as_stream(stream);
   if (decode_fast(C, n_q, n_kv, p))
     return launch_decode(p, hd, n_q / n_kv, q, k_cache, v_cache, ws_ml, ws_o, out, n_kv, L, start, scale, st);
-  int rc;
-  if (hd == 128) {
+  int rc = Q4_OK;
+  if (p.mfma) {
+    const dim3 grid(p.n_splits, n_kv, p.n_cblk), block(64 * std::max(n_q / n_kv, 4));
+    if (hd == 128)
+      hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, block, 0, st, q, q_row_stride, k_cache, v_cache, ws_ml,
+                         ws_o, C, n_q, n_kv, L, p.S, start, scale);
+    else
+      hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, block, 0, st, q, q_row_stride, k_cache, v_cache, ws_ml,
+                         ws_o, C, n_q, n_kv, L, p.S, start, scale);
+    rc = launch_status();
+  } else if (hd == 128) {
     if (p.S == 32) rc = launch_split<128, 32>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
     else if (p.S == 64) rc = launch_split<128, 64>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
     else rc = launch_split<128, 128>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);

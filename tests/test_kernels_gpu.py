@@ -93,8 +93,17 @@ def test_attn_decode_group_sizes(dev, monkeypatch, nq, nkv, hd, L, start, path):
 
 
 @pytest.mark.parametrize("Cn,start,L,nq,nkv,hd", [(256, 0, 256, 24, 8, 128), (256, 256, 512, 24, 8, 128),
-                                                  (16, 0, 64, 4, 2, 64), (8, 13, 32, 8, 2, 32 * 2), (5, 3, 64, 4, 2, 64)])
-def test_attn_prefill_chunk(dev, Cn, start, L, nq, nkv, hd):
+                                                  (16, 0, 64, 4, 2, 64), (8, 13, 32, 8, 2, 32 * 2), (5, 3, 64, 4, 2, 64),
+                                                  (100, 37, 200, 8, 8, 128), (70, 500, 600, 16, 2, 128),
+                                                  (128, 128, 384, 32, 8, 64), (33, 0, 40, 40, 8, 128)])
+@pytest.mark.parametrize("path", ["mfma", "generic"])
+def test_attn_prefill_chunk(dev, monkeypatch, Cn, start, L, nq, nkv, hd, path):
+    """Prefill chunks on the matrix-core kernel (group sizes 1-8) and on the generic split kernel
+    (forced; also the path for group sizes above 8): ragged C and L, start > 0."""
+    if path == "generic":
+        monkeypatch.setenv("Q4_ATTN_GENERIC", "1")
+    else:
+        monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
     g = torch.Generator().manual_seed(Cn + start)
     qkv_w = (nq + 2 * nkv) * hd
     qkv = torch.randn(Cn, qkv_w, generator=g)
