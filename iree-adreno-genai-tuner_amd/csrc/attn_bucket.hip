@@ -14,6 +14,7 @@
 // rule. Splits whose first key lies past every query position of the block are skipped (decode
 // reads only the valid prefix of the bucket). `start` is read on the device.
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <algorithm>
 #include <cmath>
@@ -263,7 +264,8 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
                                                          float* __restrict__ out, int n_q, int n_splits, int S,
-                                                         const int32_t* __restrict__ start_p) {
+                                                         const int32_t* __restrict__ start_p, uint16_t* __restrict__ xh,
+                                                         uint16_t* __restrict__ xl) {
   constexpr int kBatch = 32;
   constexpr int NW = HD / 64 > 0 ? HD / 64 : 1;
   __shared__ float wts[512];
@@ -301,7 +303,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   for (int j = 0; j < kBatch; ++j)
     if (j < ns) num = fmaf(wts[j], ov[j], num);
   for (int i = kBatch; i < ns; ++i) num = fmaf(wts[i], ws_o[(base + i) * HD + d], num);
-  out[(static_cast<size_t>(c) * n_q + h) * HD + d] = num / D;
+  const size_t k = (static_cast<size_t>(c) * n_q + h) * HD + d;
+  if (xh) store_x_planes(xh, xl, static_cast<int64_t>(k), num / D);  // the o-projection's x planes
+  else out[k] = num / D;
 }
 
 // ---- Decode (one query row): a register-resident split kernel and a merge that needs no position ----
@@ -838,10 +842,14 @@ extern "C" int attn_workspace_bytes(int C, int n_q, int n_kv, int hd, int L, siz
   return Q4_OK;
 }
 
-extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
-                           float* out, int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
-                           void* workspace, size_t workspace_bytes, void* stream) {
-  if (!q || !k_cache || !v_cache || !out || !start || !workspace) return Q4_ERR_NULL;
+namespace {
+// out: fp32 [C, n_q * hd]; or, with xh != nullptr (prefill only), the fp16 (hi, lo) planes of the
+// o-projection's input in place of out.
+int attn_bucket_impl(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                     uint16_t* xh, uint16_t* xl, int C, int n_q, int n_kv, int hd, int L, const int32_t* start,
+                     float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !(out || xh) || !start || !workspace) return Q4_ERR_NULL;
+  if (xh && (!xl || C == 1)) return Q4_ERR_SHAPE;
   if (int st = attn_args(C, n_q, n_kv, hd, L)) return st;
   if (q_row_stride < n_q * hd || q_row_stride % 4) return Q4_ERR_SHAPE;
   size_t need = 0;
@@ -875,8 +883,29 @@ extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_c
   }
   if (rc) return rc;
   if (hd == 128)
-    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(C * n_q), dim3(128), 0, st, ws_ml, ws_o, out, n_q, p.n_splits, p.S, start);
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(C * n_q), dim3(128), 0, st, ws_ml, ws_o, out, n_q, p.n_splits,
+                       p.S, start, xh, xl);
   else
-    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(C * n_q), dim3(64), 0, st, ws_ml, ws_o, out, n_q, p.n_splits, p.S, start);
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(C * n_q), dim3(64), 0, st, ws_ml, ws_o, out, n_q, p.n_splits,
+                       p.S, start, xh, xl);
   return launch_status();
 }
+}  // namespace
+
+extern "C" int attn_bucket(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
+                           float* out, int C, int n_q, int n_kv, int hd, int L, const int32_t* start, float scale,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out) return Q4_ERR_NULL;
+  return attn_bucket_impl(q, q_row_stride, k_cache, v_cache, out, nullptr, nullptr, C, n_q, n_kv, hd, L, start, scale,
+                          workspace, workspace_bytes, stream);
+}
+
+namespace q4 {
+int attn_bucket_planes(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
+                       uint16_t* xh, uint16_t* xl, int C, int n_q, int n_kv, int hd, int L, const int32_t* start,
+                       float scale, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!xh || !xl) return Q4_ERR_NULL;
+  return attn_bucket_impl(q, q_row_stride, k_cache, v_cache, nullptr, xh, xl, C, n_q, n_kv, hd, L, start, scale,
+                          workspace, workspace_bytes, stream);
+}
+}  // namespace q4

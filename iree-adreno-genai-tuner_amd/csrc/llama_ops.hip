@@ -6,6 +6,7 @@
 // same operation order the element-wise results are bit-identical to the CPU ops, and only the
 // reductions (sum of squares, exp) differ in the last bits.
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <cmath>
 
@@ -17,9 +18,11 @@ namespace {
 // rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
 // mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w. Rows of at
 // most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight.
+// With xh != nullptr the row goes to the fp16 (hi, lo) planes of a prefill projection instead of out.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
-                                                      const int32_t* __restrict__ row_sel) {
+                                                      const int32_t* __restrict__ row_sel,
+                                                      uint16_t* __restrict__ xh, uint16_t* __restrict__ xl) {
   // a selected row outside [0, M) is clamped (the reference's index_select would raise)
   const int64_t row = row_sel ? min(max(static_cast<int64_t>(row_sel[0]), int64_t{0}), M - 1) : blockIdx.x;
   const float* xr = x + row * D;
@@ -59,14 +62,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
       const int64_t j = threadIdx.x + i * 256;
       if (j < D / 4) {
         const float4 ww = reinterpret_cast<const float4*>(w)[j];
-        reinterpret_cast<float4*>(orow)[j] =
+        const float4 y =
             make_float4((v[i].x * r) * ww.x, (v[i].y * r) * ww.y, (v[i].z * r) * ww.z, (v[i].w * r) * ww.w);
+        if (xh) {
+          // lanes 2l and 2l + 1 hold float4s j and j + 1 (j even for lane 2l): lane 2l stores the chunk
+          const float nx = __shfl_xor(y.x, 1, 64), ny = __shfl_xor(y.y, 1, 64);
+          const float nz = __shfl_xor(y.z, 1, 64), nw = __shfl_xor(y.w, 1, 64);
+          if ((j & 1) == 0) {
+            const float e8[8] = {y.x, y.y, y.z, y.w, nx, ny, nz, nw};
+            store_x_planes8(xh, xl, (static_cast<int64_t>(blockIdx.x) * D + 4 * j) / 8, e8);
+          }
+        } else {
+          reinterpret_cast<float4*>(orow)[j] = y;
+        }
       }
     }
   } else {
     for (int64_t i = threadIdx.x; i < D; i += 256) {
       const float t = xr[i] * r;
-      orow[i] = t * w[i];
+      const float y = t * w[i];
+      if (xh) store_x_planes(xh, xl, static_cast<int64_t>(blockIdx.x) * D + i, y);
+      else orow[i] = y;
     }
   }
 }
@@ -115,18 +131,35 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, c
   }
 }
 
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  const float e = expf(-g);
+  const float den = 1.0f + e;
+  const float sg = g / den;
+  return sg * u;
+}
+
 // silu(g) * u with silu(x) = x / (1 + exp(-x)) (F.silu), gu = [M, 2 * inter] (gate then up).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu, float* __restrict__ out,
                                                        int64_t M, int64_t inter) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (t >= M * inter) return;
   const int64_t m = t / inter, i = t % inter;
-  const float g = gu[m * 2 * inter + i];
-  const float u = gu[m * 2 * inter + inter + i];
-  const float e = expf(-g);
-  const float den = 1.0f + e;
-  const float sg = g / den;
-  out[t] = sg * u;
+  out[t] = silu_mul1(gu[m * 2 * inter + i], gu[m * 2 * inter + inter + i]);
+}
+
+// The same into the fp16 (hi, lo) planes of the down projection: one thread per 8-element chunk
+// (inter % 8 == 0), two 16-byte loads of gate and of up, one 16-byte store per plane.
+__global__ __launch_bounds__(256) void silu_mul_planes_kernel(const float* __restrict__ gu, uint16_t* __restrict__ xh,
+                                                              uint16_t* __restrict__ xl, int64_t M, int64_t inter) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // chunk of the [M, inter] result
+  if (c >= M * inter / 8) return;
+  const int64_t m = (8 * c) / inter, i = (8 * c) % inter;
+  const float4* gp = reinterpret_cast<const float4*>(gu + m * 2 * inter + i);
+  const float4* up = reinterpret_cast<const float4*>(gu + m * 2 * inter + inter + i);
+  const float4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
+  const float e8[8] = {silu_mul1(g0.x, u0.x), silu_mul1(g0.y, u0.y), silu_mul1(g0.z, u0.z), silu_mul1(g0.w, u0.w),
+                       silu_mul1(g1.x, u1.x), silu_mul1(g1.y, u1.y), silu_mul1(g1.z, u1.z), silu_mul1(g1.w, u1.w)};
+  store_x_planes8(xh, xl, c, e8);
 }
 
 // argmax with torch.argmax semantics: the first index of the maximum; a NaN counts as the maximum
@@ -208,7 +241,8 @@ extern "C" int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M
   if (M <= 0 || D <= 0) return Q4_ERR_SHAPE;
   if (D % 4 == 0 && (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))) return Q4_ERR_ALIGN;
   const unsigned grid = row ? 1u : static_cast<unsigned>(M);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row,
+                     nullptr, nullptr);
   return launch_status();
 }
 
@@ -229,6 +263,29 @@ extern "C" int silu_mul_f32(const float* gu, float* out, int64_t M, int64_t inte
                      as_stream(stream), gu, out, M, inter);
   return launch_status();
 }
+
+namespace q4 {
+
+int rmsnorm_planes(const float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
+                   hipStream_t st) {
+  if (!x || !w || !xh || !xl) return Q4_ERR_NULL;
+  if (M <= 0 || D <= 0 || D % 8) return Q4_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
+                     nullptr, xh, xl);
+  return launch_status();
+}
+
+int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st) {
+  if (!gu || !xh || !xl) return Q4_ERR_NULL;
+  if (M <= 0 || inter <= 0 || inter % 8) return Q4_ERR_SHAPE;
+  if (!aligned(gu, 16) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
+  hipLaunchKernelGGL(silu_mul_planes_kernel, dim3(static_cast<unsigned>((M * inter / 8 + 255) / 256)), dim3(256), 0,
+                     st, gu, xh, xl, M, inter);
+  return launch_status();
+}
+
+}  // namespace q4
 
 extern "C" int argmax_workspace_bytes(int64_t V, size_t* bytes) {
   if (!bytes) return Q4_ERR_NULL;

@@ -83,4 +83,35 @@ __device__ __forceinline__ float segment_sum_to_last(float v) {
   return v;
 }
 
+// The fp16 (hi, lo) planes a prefill projection takes as its x operand: hi = fp16(v) (round to
+// nearest even), lo = fp16(v - hi); element k of a row sits at position (k & ~7) | 2 (k & 3) |
+// ((k >> 2) & 1), i.e. each 8-element chunk in the order (0, 4, 1, 5, 2, 6, 3, 7), the k order in
+// which the projection decodes a packed int4 word.
+__device__ __forceinline__ void store_x_planes(uint16_t* __restrict__ xh, uint16_t* __restrict__ xl, int64_t k,
+                                               float v) {
+  const _Float16 hi = static_cast<_Float16>(v);
+  const _Float16 lo = static_cast<_Float16>(v - static_cast<float>(hi));
+  const int64_t p = (k & ~int64_t{7}) | ((k & 3) << 1) | ((k >> 2) & 1);
+  xh[p] = __builtin_bit_cast(uint16_t, hi);
+  xl[p] = __builtin_bit_cast(uint16_t, lo);
+}
+
+// Eight consecutive elements 8c .. 8c + 7 of a row (v[i] = element 8c + i) as one 16-byte store per
+// plane (same values and layout as eight store_x_planes calls).
+__device__ __forceinline__ void store_x_planes8(uint16_t* __restrict__ xh, uint16_t* __restrict__ xl, int64_t c,
+                                                const float (&v)[8]) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float a = v[p], b = v[p + 4];  // positions 2p and 2p + 1 hold elements p and p + 4
+    const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+    const _Float16 la = static_cast<_Float16>(a - static_cast<float>(ha));
+    const _Float16 lb = static_cast<_Float16>(b - static_cast<float>(hb));
+    h[p] = __builtin_bit_cast(uint16_t, ha) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+    l[p] = __builtin_bit_cast(uint16_t, la) | (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lb)) << 16);
+  }
+  reinterpret_cast<uint4*>(xh)[c] = make_uint4(h[0], h[1], h[2], h[3]);
+  reinterpret_cast<uint4*>(xl)[c] = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
 }  // namespace q4

@@ -15,6 +15,7 @@
 // double-buffered LDS staging with 16-byte row padding, raw buffer loads (out-of-range = zeros).
 // Requires K % 64 == 0 and group % 32 == 0 (the host checks); |x| must stay below 65504 (fp16 range).
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <cstdlib>
 
@@ -608,19 +609,13 @@ int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_
 
 int q4_linear_ws_num_tiles() { return kNumLinWs; }
 
-// Fixed rule from a sweep of every entry over the 3B prefill shapes at M = 128, 256 and 1024 (graph
-// replays on one MI355X): the 32x64 k-split tile while it gives at most 768 workgroups (every
-// M <= 256 chunk of the 3072-, 5120- and 8192-wide projections), else 64x64. Q4_LINEAR_CFG overrides.
-int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
-                        int64_t N, int64_t K, int group, void* ws, hipStream_t st) {
-  // the pipelined kernel indexes groups by shifts: other group sizes take the workspace-free kernel
-  if (group & (group - 1)) return q4_linear_launch(x, M, qw, sc, y, res, N, K, group, -1, st);
-  uint16_t* xh = static_cast<uint16_t*>(ws);
-  uint16_t* xl = xh + M * K;
-  const int64_t chunks = M * K / 8;
-  hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, st, x, xh, xl,
-                     chunks);
-  if (int e = launch_status()) return e;
+// The pipelined GEMM on x given as fp16 (hi, lo) planes (store_x_planes layout, [M, K] each);
+// power-of-two groups only. Tile rule from a sweep of every entry over the 3B prefill shapes at
+// M = 128, 256 and 1024 (graph replays on one MI355X): the 32x64 k-split tile while it gives at most
+// 768 workgroups (every M <= 256 chunk of the 3072-, 5120- and 8192-wide projections), else 64x64.
+// Q4_LINEAR_CFG overrides.
+int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
+                     float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st) {
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
@@ -635,6 +630,19 @@ int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint
   hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
                      (int)M, (int)N, (int)K, group, tiles_n);
   return launch_status();
+}
+
+int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
+                        int64_t N, int64_t K, int group, void* ws, hipStream_t st) {
+  // the pipelined kernel indexes groups by shifts: other group sizes take the workspace-free kernel
+  if (group & (group - 1)) return q4_linear_launch(x, M, qw, sc, y, res, N, K, group, -1, st);
+  uint16_t* xh = static_cast<uint16_t*>(ws);
+  uint16_t* xl = xh + M * K;
+  const int64_t chunks = M * K / 8;
+  hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, st, x, xh, xl,
+                     chunks);
+  if (int e = launch_status()) return e;
+  return q4_linear_planes(xh, xl, M, qw, sc, y, res, N, K, group, st);
 }
 
 }  // namespace q4

@@ -13,12 +13,15 @@
 // then x = rms_norm(h[last], ln_f), logits = x E^T (tied int4 embedding), next = argmax(logits).
 // Projections: C == 1 -> q4_gemv (fp32 in/out, residual fused; norms, RoPE + cache writes and SwiGLU
 // fused into the GEMVs); C > 1 -> q4_linear (fused int4 MFMA GEMM with split-fp16 activations and
-// per-group fp32 scales, residual fused; its fp16 x planes live in the step workspace).
+// per-group fp32 scales, residual fused; its fp16 x planes live in the step workspace and are written
+// directly by the norm, attention-merge and SwiGLU kernels that produce them).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstddef>
 
+#include "q4_internal.h"
 #include "q4llm.h"
 
 namespace {
@@ -145,6 +148,13 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   // norm and SwiGLU in its epilogue; down-projection + residual; after the layers the LM head GEMV
   // takes the final norm in its x staging. Prefill uses the separate kernels.
   const bool fused = C == 1 && gemv_fusable(D, m->group);
+  // Prefill with a power-of-two group: the norms, the attention merge and SwiGLU write their results
+  // straight as the fp16 (hi, lo) planes the following projection reads (in the lin workspace).
+  const int kmax = std::max(D, std::max(nq_w, m->inter));
+  const bool planes = C > 1 && (m->group & (m->group - 1)) == 0 && D % 8 == 0 && nq_w % 8 == 0 && m->inter % 8 == 0;
+  uint16_t* xh = static_cast<uint16_t*>(lin_ws);
+  uint16_t* xl = xh + static_cast<size_t>(C) * kmax;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
@@ -154,17 +164,32 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
       const q4_rope_kv rope{m->cos_t, m->sin_t, kc, vc, start, nh, nkv, hd, m->max_ctx};
       Q4_TRY(q4_gemv_epilogue(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV, &rope, qkv,
                               qkv_w, D, m->group, stream));
+    } else if (planes) {
+      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st));
+      Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, lin_ws, lo.lin_bytes, stream));
       Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     }
-    Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
-    Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, lin_ws, lo.lin_bytes, stream));
+    if (planes) {
+      Q4_TRY(q4::attn_bucket_planes(qkv, qkv_w, kc, vc, xh, xl, C, nh, nkv, hd, L, start, scale, attn_ws,
+                                    lo.attn_bytes, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st));
+    } else {
+      Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
+      Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, lin_ws, lo.lin_bytes, stream));
+    }
     if (fused) {
       Q4_TRY(q4_gemv_epilogue(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU, nullptr, act,
                               2 * m->inter, D, m->group, stream));
       Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
+    } else if (planes) {
+      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_post, xh, xl, C, D, m->eps, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st));
+      Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, lin_ws, lo.lin_bytes, stream));
