@@ -37,6 +37,21 @@ constexpr int kWave = 64;
 // Device helpers
 // ------------------------------------------------------------------------------------------
 
+// The fp16 exponent patterns that int4 nibble masks are OR'ed with (nibble -> 1024 + n or 64 + n),
+// held in VGPRs. gfx9's three-operand encoding takes no literal and reads at most one SGPR, so with
+// the mask and the pattern both constants the compiler splits (w & mask) | pattern into an AND and
+// an OR; with the pattern in a VGPR it is one v_and_or_b32 (mask in an SGPR).
+struct F16Magic {
+  uint32_t e1024, e64;  // 0x6400 = 1024.0 and 0x5400 = 64.0 in both halves
+};
+
+__device__ __forceinline__ F16Magic f16_magic() {
+  F16Magic m;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(m.e1024));
+  asm("v_mov_b32 %0, 0x54005400" : "=v"(m.e64));
+  return m;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

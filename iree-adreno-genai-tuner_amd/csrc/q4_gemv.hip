@@ -121,22 +121,8 @@ __device__ __forceinline__ XChunkF16 x_chunk_f16(const uint4* __restrict__ xs, i
   return x;
 }
 
-// The fp16 exponent patterns that the nibble masks are OR'ed with, held in VGPRs. gfx9's
-// three-operand encoding takes no literal and reads at most one SGPR, so with the mask and the
-// pattern both constants the compiler splits (w & mask) | pattern into an AND and an OR; with the
-// pattern in a VGPR it is one v_and_or_b32 (mask in an SGPR): 9 instead of 13 VALU operations per
-// 8 nibbles.
-struct F16Magic {
-  uint32_t e1024, e64;  // 0x6400 = 1024.0 and 0x5400 = 64.0 in both halves
-};
-
-__device__ __forceinline__ F16Magic f16_magic() {
-  F16Magic m;
-  asm("v_mov_b32 %0, 0x64006400" : "=v"(m.e1024));
-  asm("v_mov_b32 %0, 0x54005400" : "=v"(m.e64));
-  return m;
-}
-
+// 9 VALU operations per 8 nibbles: one shift, four v_and_or_b32 (exponent patterns from F16Magic),
+// four v_dot2_f32_f16.
 __device__ __forceinline__ float dot_chunk_f16(const uint4& w, const XChunkF16& x, const F16Magic& mg) {
   float t = 0.0f;
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};

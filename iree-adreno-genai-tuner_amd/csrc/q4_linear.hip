@@ -301,14 +301,19 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float* __restrict__ 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // Packed word of 8 nibbles (k = 8c + b at nibble b) -> the fp16 operand (n_b - 8) in k order
-// (0, 4, 1, 5, 2, 6, 3, 7). Exact: 1024 + n is an fp16 integer and so is n - 8.
-__device__ __forceinline__ half8 nibbles_to_half8(uint32_t w) {
-  const half2v bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-  half2v p[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    p[i] = __builtin_bit_cast(half2v, ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u) + bias;
-  return half8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+// (0, 4, 1, 5, 2, 6, 3, 7). Nibbles 0 and 4 (and 2 and 6 after a shift by 8) sit in the low
+// mantissa bits and become 1024 + n under exponent 0x6400; nibbles 1 and 5 (3 and 7) sit 4 bits
+// higher, where exponent 0x5400 makes them 64 + n. One packed add of -1032 or -72 then gives
+// n - 8, exactly (all values are small fp16 integers). 9 VALU operations per word.
+__device__ __forceinline__ half8 nibbles_to_half8(uint32_t w, const F16Magic& mg) {
+  const half2v b1024 = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+  const half2v b64 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+  const uint32_t w8 = w >> 8;
+  const half2v p0 = __builtin_bit_cast(half2v, (w & 0x000F000Fu) | mg.e1024) + b1024;   // n0, n4
+  const half2v p1 = __builtin_bit_cast(half2v, (w & 0x00F000F0u) | mg.e64) + b64;       // n1, n5
+  const half2v p2 = __builtin_bit_cast(half2v, (w8 & 0x000F000Fu) | mg.e1024) + b1024;  // n2, n6
+  const half2v p3 = __builtin_bit_cast(half2v, (w8 & 0x00F000F0u) | mg.e64) + b64;      // n3, n7
+  return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 template <int BM, int BN, int WM, int WN, int NST, int KS>
@@ -450,6 +455,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const unsigned char* sw = sl + BM * G::kXRow;
     const unsigned char* ss = sw + BN * G::kWRow;
     const int k0 = kt * 64;
+    const F16Magic mg = f16_magic();
     // All operand reads of the step first (x_hi, x_lo and the nibble words of the 4 16-k steps), so the
     // LDS latency is paid once per step instead of once per 16-k step.
     half8 fh[KK][G::TM], fl[KK][G::TM];
@@ -473,7 +479,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
       const int kk = ks * KK + q;
       half8 fb[G::TN];
 #pragma unroll
-      for (int j = 0; j < G::TN; ++j) fb[j] = nibbles_to_half8(fw[q][j]);
+      for (int j = 0; j < G::TN; ++j) fb[j] = nibbles_to_half8(fw[q][j], mg);
 #pragma unroll
       for (int i = 0; i < G::TM; ++i)
 #pragma unroll
