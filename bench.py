@@ -37,10 +37,10 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 2 ** 20
 
 # HBM bytes per 5120x3072 launch from rocprofv3 counter passes over this bench's GEMV leg
-# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4023.0 KiB x 1.995 (the factor that maps
+# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4020.0 KiB x 1.995 (the factor that maps
 # FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 20.0 KiB x 1.0.
 # Counters cannot be read inside a timed run, so the figure is carried here with its source.
-GEMV_TRAFFIC_BYTES_5120x3072 = 8_238_986
+GEMV_TRAFFIC_BYTES_5120x3072 = 8_232_858
 
 
 def log(*a):

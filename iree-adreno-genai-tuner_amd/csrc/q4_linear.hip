@@ -570,6 +570,10 @@ constexpr LinWsTile kLinWsTiles[] = {
     {128, 64, 2, 2, 4, 2},   // 3: 8 waves: 4 tiles of 64x32, k-split over 2
     {32, 32, 1, 1, 4, 2},    // 4: 2 waves: one 32x32 tile, k-split over 2
     {128, 128, 2, 2, 4, 1},  // 5: 4 waves of 64x64 (152 KB)
+    {64, 128, 2, 2, 4, 1},   // 6: 4 waves of 32x64
+    {64, 128, 2, 2, 4, 2},   // 7: 8 waves: 4 tiles of 32x64, k-split over 2
+    {32, 128, 1, 2, 4, 2},   // 8: 4 waves: 2 tiles of 32x64, k-split over 2
+    {128, 64, 2, 2, 4, 1},   // 9: 4 waves of 64x32
 };
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
                          int, int, int, int);
@@ -583,10 +587,12 @@ constexpr size_t lin_ws_lds() {
   constexpr LinWsTile t = kLinWsTiles[I];
   return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
 }
-constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(),
-                                 lin_ws_fn<3>(), lin_ws_fn<4>(), lin_ws_fn<5>()};
-constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(),
-                                lin_ws_lds<3>(), lin_ws_lds<4>(), lin_ws_lds<5>()};
+constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(), lin_ws_fn<3>(), lin_ws_fn<4>(),
+                                 lin_ws_fn<5>(), lin_ws_fn<6>(), lin_ws_fn<7>(), lin_ws_fn<8>(), lin_ws_fn<9>()};
+constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(), lin_ws_lds<3>(), lin_ws_lds<4>(),
+                                lin_ws_lds<5>(), lin_ws_lds<6>(), lin_ws_lds<7>(), lin_ws_lds<8>(), lin_ws_lds<9>()};
+static_assert(sizeof(kLinWsFns) / sizeof(kLinWsFns[0]) == sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]),
+              "one kernel per tile entry");
 constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
 
 }  // namespace
