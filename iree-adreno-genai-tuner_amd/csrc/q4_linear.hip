@@ -324,12 +324,13 @@ struct LinWsCfg {
   static constexpr int kWRow = 32;                         // bytes per weight row per stage (64 nibbles)
   static constexpr int kSBlk = (BN + 63) / 64;             // 64-column blocks of the scale slots
   static constexpr int kStage = 2 * BM * kXRow + BN * kWRow + 2 * kSBlk * 256;  // + 2 scale slots
-  static constexpr int kAI = BM / 8 / kWaves;             // x direct loads per wave, per plane
+  static constexpr int kAI = (BM / 8 + kWaves - 1) / kWaves;  // x direct loads per wave, per plane
   static constexpr int kBI = (BN / 32 + kWaves - 1) / kWaves;  // weight direct loads per wave (32 rows each)
   static constexpr int kSI = (2 * kSBlk + kWaves - 1) / kWaves;  // scale direct loads per wave
   static constexpr int kLPW = 2 * kAI + kBI + kSI;
   static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + 1024;  // + junk for spare loads
-  static_assert(TM >= 1 && TN >= 1 && kAI * 8 * kWaves == BM, "tile shape");
+  static_assert(TM >= 1 && TN >= 1 && WTM * WM == BM && WTN * WN == BN && BM % 32 == 0 && BN % 32 == 0,
+                "tile shape");
   static_assert(NST >= 2 && NST <= 8 && kLPW * (NST - 1) < 64, "stages: vmcnt holds at most 63");
   static_assert(KS == 1 || KS == 2 || KS == 4, "k split over 1, 2 or 4 wave groups");
   static constexpr size_t kRed = static_cast<size_t>(KS - 1) * WM * WN * TM * TN * 16 * 64 * 4;
@@ -359,15 +360,20 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(QW, static_cast<uint32_t>(N) * (K / 2));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(SC, (static_cast<uint32_t>(N) * spr * 2u + 3u) & ~3u);
 
-  // x planes: instruction j fills rows 8b..8b+7 (b = wave + j * kWaves) of a 128-byte-row plane; the
-  // lane for slot (lane % 8) of row r = 8b + lane / 8 fetches chunk (lane % 8) ^ ((r >> 1) & 7).
+  // x planes: instruction j fills rows 8b..8b+7 (b = wave + j * kWaves < BM / 8) of a 128-byte-row
+  // plane; the lane for slot (lane % 8) of row r = 8b + lane / 8 fetches chunk (lane % 8) ^ ((r >> 1) & 7).
+  // When the waves do not divide BM / 8, the spare instructions load nothing into the junk area, so
+  // every wave issues the same number of loads per step.
   uint32_t xoff[G::kAI];
   int xchunk[G::kAI];
+  bool xreal[G::kAI];
 #pragma unroll
   for (int j = 0; j < G::kAI; ++j) {
-    const int r = 8 * (wave + j * G::kWaves) + (lane >> 3);
+    const int b = wave + j * G::kWaves;
+    const int r = 8 * b + (lane >> 3);
+    xreal[j] = b < BM / 8;
     xchunk[j] = (lane & 7) ^ ((r >> 1) & 7);
-    xoff[j] = m0 + r < M ? static_cast<uint32_t>(m0 + r) * K * 2u + xchunk[j] * 16u : kOOBw;
+    xoff[j] = xreal[j] && m0 + r < M ? static_cast<uint32_t>(m0 + r) * K * 2u + xchunk[j] * 16u : kOOBw;
   }
   // weights: instruction j fills rows 32b..32b+31 (b = wave + j * kWaves < BN / 32) with 32-byte rows,
   // lane -> (row lane / 2, half lane % 2); spare instructions load nothing into a junk area.
@@ -393,8 +399,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
 #pragma unroll
     for (int j = 0; j < G::kAI; ++j) {
       const uint32_t off = kin && xoff[j] != kOOBw ? xoff[j] + k0 * 2u : kOOBw;
-      load_lds16(hr, sh + (wave + j * G::kWaves) * 1024, off);
-      load_lds16(lr, sl + (wave + j * G::kWaves) * 1024, off);
+      load_lds16(hr, xreal[j] ? sh + (wave + j * G::kWaves) * 1024 : junk, off);
+      load_lds16(lr, xreal[j] ? sl + (wave + j * G::kWaves) * 1024 : junk, off);
     }
 #pragma unroll
     for (int j = 0; j < G::kBI; ++j)
@@ -574,6 +580,13 @@ constexpr LinWsTile kLinWsTiles[] = {
     {64, 128, 2, 2, 4, 2},   // 7: 8 waves: 4 tiles of 32x64, k-split over 2
     {32, 128, 1, 2, 4, 2},   // 8: 4 waves: 2 tiles of 32x64, k-split over 2
     {128, 64, 2, 2, 4, 1},   // 9: 4 waves of 64x32
+    // one workgroup per CU at M = 256 for N = 5120, 16384 and 3072 (x re-read over fewer column tiles)
+    {32, 160, 1, 5, 4, 1},   // 10: 5 waves of 32x32
+    {32, 160, 1, 5, 4, 2},   // 11: 10 waves, k-split over 2
+    {64, 256, 2, 4, 4, 1},   // 12: 8 waves of 32x64
+    {64, 256, 1, 4, 4, 1},   // 13: 4 waves of 64x64
+    {32, 96, 1, 3, 4, 2},    // 14: 6 waves: 3 tiles of 32x32, k-split over 2
+    {32, 96, 1, 3, 4, 1},    // 15: 3 waves of 32x32
 };
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
                          int, int, int, int);
@@ -587,10 +600,14 @@ constexpr size_t lin_ws_lds() {
   constexpr LinWsTile t = kLinWsTiles[I];
   return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
 }
-constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>(), lin_ws_fn<3>(), lin_ws_fn<4>(),
-                                 lin_ws_fn<5>(), lin_ws_fn<6>(), lin_ws_fn<7>(), lin_ws_fn<8>(), lin_ws_fn<9>()};
-constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(), lin_ws_lds<3>(), lin_ws_lds<4>(),
-                                lin_ws_lds<5>(), lin_ws_lds<6>(), lin_ws_lds<7>(), lin_ws_lds<8>(), lin_ws_lds<9>()};
+constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(),  lin_ws_fn<1>(),  lin_ws_fn<2>(),  lin_ws_fn<3>(),
+                                 lin_ws_fn<4>(),  lin_ws_fn<5>(),  lin_ws_fn<6>(),  lin_ws_fn<7>(),
+                                 lin_ws_fn<8>(),  lin_ws_fn<9>(),  lin_ws_fn<10>(), lin_ws_fn<11>(),
+                                 lin_ws_fn<12>(), lin_ws_fn<13>(), lin_ws_fn<14>(), lin_ws_fn<15>()};
+constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(),  lin_ws_lds<1>(),  lin_ws_lds<2>(),  lin_ws_lds<3>(),
+                                lin_ws_lds<4>(),  lin_ws_lds<5>(),  lin_ws_lds<6>(),  lin_ws_lds<7>(),
+                                lin_ws_lds<8>(),  lin_ws_lds<9>(),  lin_ws_lds<10>(), lin_ws_lds<11>(),
+                                lin_ws_lds<12>(), lin_ws_lds<13>(), lin_ws_lds<14>(), lin_ws_lds<15>()};
 static_assert(sizeof(kLinWsFns) / sizeof(kLinWsFns[0]) == sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]),
               "one kernel per tile entry");
 constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
@@ -631,7 +648,14 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
-  if (ti < 0) ti = ((M + 31) / 32) * ((N + 63) / 64) <= 768 ? 1 : 0;
+  // Rule from a sweep at M = 128, 256, 1024: the 32x64 k-split tile while it gives <= 768 workgroups,
+  // else 64x64; and 64x256 when, at M <= 256, it alone gives one workgroup per CU (the gate/up
+  // projection of a 256-row chunk: 256x16384x3072 82 -> 69 us, x re-read over 4x fewer column tiles).
+  if (ti < 0) {
+    const int64_t wide = ((M + 63) / 64) * ((N + 255) / 256);
+    if (M <= 256 && wide >= 256) ti = 12;
+    else ti = ((M + 31) / 32) * ((N + 63) / 64) <= 768 ? 1 : 0;
+  }
   const LinWsTile& t = kLinWsTiles[ti];
   const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
   const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
