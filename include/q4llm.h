@@ -229,7 +229,9 @@ int q4llm_step_workspace_bytes(const q4llm_model* m, int C, int L, size_t* bytes
  * pointers (k0, v0, k1, v1, ...) each [max_ctx, n_kv, head_dim] fp16 written in place at
  * start..start+C-1; attention reads cache[:L]. Writes the greedy next token (int32) to next[0]
  * and, if logits != NULL, the [vocab] fp32 logits of row `last`. The host checks C, L against
- * max_ctx; start + C <= L is the caller's schedule contract (llm_runner.c:143-149). */
+ * max_ctx; start + C <= L is the caller's schedule contract (llm_runner.c:143-149). The tokens are
+ * read by the step's first kernel and next is written by its last, so for C == 1 `tokens` may be
+ * `next` itself (a decode loop that feeds each token back on the device). */
 int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start,
                const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
                void* workspace, size_t workspace_bytes, void* stream);

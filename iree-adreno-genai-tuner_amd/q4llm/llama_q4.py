@@ -349,15 +349,22 @@ class LlamaQ4(nn.Module):
 
 
 class _StepGraph:
-    """One (C, L) step captured into a HIP graph; inputs are copied into static device buffers."""
+    """One (C, L) step captured into a HIP graph; inputs are copied into static device buffers.
+
+    Decode graphs (C == 1) feed themselves: the token buffer is the `next` buffer (q4llm_step reads
+    the tokens in its first kernel and writes next in its last), and the graph ends by adding 1 to
+    `start`. After a replay the device inputs therefore already hold (start + 1, next token), which
+    is what the runner's following decode call passes, so the runner only writes them after a
+    bucket switch (`feeds_back`)."""
 
     def __init__(self, model: LlamaQ4, Cn, L, caches, with_logits):
         dev = model.device
         self.model, self.C, self.L = model, Cn, L
-        self.tokens = torch.zeros(Cn, dtype=torch.int32, device=dev)
+        self.feeds_back = Cn == 1
         self.start = torch.zeros(1, dtype=torch.int32, device=dev)
         self.last = torch.zeros(1, dtype=torch.int32, device=dev)
         self.next = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tokens = self.next if self.feeds_back else torch.zeros(Cn, dtype=torch.int32, device=dev)
         self.logits = torch.empty(1, model.embed.vocab, dtype=torch.float32, device=dev) if with_logits else None
         self.cache_arr = model._cache_ptrs(caches)
         self.caches = caches
@@ -371,6 +378,8 @@ class _StepGraph:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=s):
             model._raw_step(self.tokens, Cn, self.start, self.last, self.cache_arr, L, self.next, self.logits)
+            if self.feeds_back:
+                self.start.add_(1)
 
     def set_inputs(self, tokens, start, last):
         self.tokens.copy_(torch.as_tensor(tokens, dtype=torch.int32).reshape(-1), non_blocking=False)
