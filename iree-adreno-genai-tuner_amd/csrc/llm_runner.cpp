@@ -255,12 +255,20 @@ void* need(Packed& pk, const std::string& name) {
 // Entry points: one graph-captured q4llm_step per (C, L)
 // ------------------------------------------------------------------------------------------------
 
+// Decode entry points (C == 1) feed themselves: their token buffer is their `next` buffer (q4llm_step
+// reads the tokens in its first kernel and writes next in its last) and the graph ends by adding 1
+// to start, so after a call the device inputs already hold what the following decode call passes;
+// `call` then skips the host-to-device copy.
+__global__ void advance_start_kernel(int32_t* start) { start[0] += 1; }
+
 struct EntryPoint {
   int C = 0, L = 0;
   int32_t *tokens = nullptr, *start = nullptr, *last = nullptr, *next = nullptr;  // device
   void* ws = nullptr;
   size_t ws_bytes = 0;
   hipGraphExec_t exec = nullptr;
+  bool fed = false;  // decode only: the device holds (fed_start, fed_token, last = 0) as inputs
+  int32_t fed_start = 0, fed_token = 0;
 };
 
 struct Runner {
@@ -289,6 +297,7 @@ struct Runner {
     e.start = e.tokens + C;
     e.last = e.start + 1;
     e.next = e.last + 1;
+    if (C == 1) e.tokens = e.next;
     Q4_OK_OR_DIE(q4llm_step_workspace_bytes(&model, C, L, &e.ws_bytes));
     HIP_OK(hipMalloc(&e.ws, e.ws_bytes));
     HIP_OK(hipMemset(e.ws, 0, e.ws_bytes));
@@ -297,6 +306,10 @@ struct Runner {
     hipGraph_t g = nullptr;
     HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     raw_step(e);
+    if (C == 1) {
+      hipLaunchKernelGGL(advance_start_kernel, dim3(1), dim3(1), 0, stream, e.start);
+      HIP_OK(hipGetLastError());
+    }
     HIP_OK(hipStreamEndCapture(stream, &g));
     HIP_OK(hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0));
     HIP_OK(hipGraphDestroy(g));
@@ -311,14 +324,30 @@ struct Runner {
       host_cap = C + 3;
       HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&host), sizeof(int32_t) * host_cap, hipHostMallocDefault));
     }
-    for (int i = 0; i < C; ++i) host[i] = i < n ? tokens[i] : 0;
-    host[C] = start;
-    host[C + 1] = last;
-    HIP_OK(hipMemcpyAsync(e.tokens, host, sizeof(int32_t) * (C + 2), hipMemcpyHostToDevice, stream));
+    const bool fed = C == 1 && e.fed && e.fed_start == start && e.fed_token == tokens[0] && last == 0;
+    if (!fed) {
+      if (C == 1) {  // layout [start, last, next = tokens]
+        host[0] = start;
+        host[1] = last;
+        host[2] = n > 0 ? tokens[0] : 0;
+        HIP_OK(hipMemcpyAsync(e.start, host, sizeof(int32_t) * 3, hipMemcpyHostToDevice, stream));
+      } else {
+        for (int i = 0; i < C; ++i) host[i] = i < n ? tokens[i] : 0;
+        host[C] = start;
+        host[C + 1] = last;
+        HIP_OK(hipMemcpyAsync(e.tokens, host, sizeof(int32_t) * (C + 2), hipMemcpyHostToDevice, stream));
+      }
+    }
     HIP_OK(hipGraphLaunch(e.exec, stream));
     HIP_OK(hipMemcpyAsync(host + C + 2, e.next, sizeof(int32_t), hipMemcpyDeviceToHost, stream));
     HIP_OK(hipStreamSynchronize(stream));
-    return host[C + 2];
+    const int32_t out = host[C + 2];
+    if (C == 1) {
+      e.fed = true;
+      e.fed_start = start + 1;
+      e.fed_token = out;
+    }
+    return out;
   }
 };
 
