@@ -17,7 +17,8 @@ namespace {
 
 // rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
 // mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w. Rows of at
-// most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight.
+// most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight; the
+// norm weights are loaded with them, so no memory round trip follows the row reduction.
 // With xh != nullptr the row goes to the fp16 (hi, lo) planes of a prefill projection instead of out.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
@@ -29,13 +30,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   float* orow = out + static_cast<int64_t>(blockIdx.x) * D;
   constexpr int kV = 4;
   const bool vec = D % 4 == 0 && D <= 4 * 256 * kV;
-  float4 v[kV];
+  float4 v[kV], wv[kV];
   float s = 0.0f;
   if (vec) {
 #pragma unroll
     for (int i = 0; i < kV; ++i) {
       const int64_t j = threadIdx.x + i * 256;
       v[i] = j < D / 4 ? reinterpret_cast<const float4*>(xr)[j] : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const int64_t j = threadIdx.x + i * 256;
+      wv[i] = j < D / 4 ? reinterpret_cast<const float4*>(w)[j] : make_float4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kV; ++i) {
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     for (int i = 0; i < kV; ++i) {
       const int64_t j = threadIdx.x + i * 256;
       if (j < D / 4) {
-        const float4 ww = reinterpret_cast<const float4*>(w)[j];
+        const float4 ww = wv[i];
         const float4 y =
             make_float4((v[i].x * r) * ww.x, (v[i].y * r) * ww.y, (v[i].z * r) * ww.z, (v[i].w * r) * ww.w);
         if (xh) {
@@ -128,6 +134,64 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, c
     uint16_t* dst = vc + (static_cast<int64_t>(pos) * n_kv + (head - n_q - n_kv)) * hd;
     dst[d] = float_to_half_bits(x1);
     dst[d + half] = float_to_half_bits(x2);
+  }
+}
+
+// The same for hd % 8 == 0 with four consecutive d per thread: 16-byte loads of the row halves and
+// the cos / sin entries, 16-byte row stores, 8-byte cache stores; the row loads are issued before
+// the position is known. Same expressions, so the same bits as rope_kv_kernel.
+__global__ __launch_bounds__(256) void rope_kv4_kernel(float* __restrict__ qkv, const float* __restrict__ cos_t,
+                                                       const float* __restrict__ sin_t, uint16_t* __restrict__ kc,
+                                                       uint16_t* __restrict__ vc, int C, int n_q, int n_kv, int hd,
+                                                       int max_ctx, const int32_t* __restrict__ start_p) {
+  const int half = hd / 2, q4 = half / 4;
+  const int heads = n_q + 2 * n_kv;
+  const int64_t total = static_cast<int64_t>(C) * heads * q4;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int d = static_cast<int>(t % q4) * 4;
+  const int head = static_cast<int>((t / q4) % heads);
+  const int c = static_cast<int>(t / (static_cast<int64_t>(q4) * heads));
+  float* row = qkv + (static_cast<int64_t>(c) * heads + head) * hd;
+  const float4 x1 = *reinterpret_cast<const float4*>(row + d);
+  const float4 x2 = *reinterpret_cast<const float4*>(row + d + half);
+  const int pos = start_p[0] + c;
+  if (pos < 0 || pos >= max_ctx) return;
+  auto half4 = [](float a, float b, float c4, float e) {
+    return make_uint2(static_cast<uint32_t>(float_to_half_bits(a)) | (static_cast<uint32_t>(float_to_half_bits(b)) << 16),
+                      static_cast<uint32_t>(float_to_half_bits(c4)) | (static_cast<uint32_t>(float_to_half_bits(e)) << 16));
+  };
+  if (head < n_q + n_kv) {  // q or k: rotate
+    const float* cp = cos_t + static_cast<int64_t>(pos) * hd;
+    const float* sp = sin_t + static_cast<int64_t>(pos) * hd;
+    const float4 c1 = *reinterpret_cast<const float4*>(cp + d), s1 = *reinterpret_cast<const float4*>(sp + d);
+    const float4 c2 = *reinterpret_cast<const float4*>(cp + d + half);
+    const float4 s2 = *reinterpret_cast<const float4*>(sp + d + half);
+    auto rot_lo = [](float a1, float a2, float cc, float ss) {
+      const float a = a1 * cc;
+      const float b = (-a2) * ss;
+      return a + b;
+    };
+    auto rot_hi = [](float a1, float a2, float cc, float ss) {
+      const float e = a2 * cc;
+      const float f = a1 * ss;
+      return e + f;
+    };
+    const float4 lo = make_float4(rot_lo(x1.x, x2.x, c1.x, s1.x), rot_lo(x1.y, x2.y, c1.y, s1.y),
+                                  rot_lo(x1.z, x2.z, c1.z, s1.z), rot_lo(x1.w, x2.w, c1.w, s1.w));
+    const float4 hi = make_float4(rot_hi(x1.x, x2.x, c2.x, s2.x), rot_hi(x1.y, x2.y, c2.y, s2.y),
+                                  rot_hi(x1.z, x2.z, c2.z, s2.z), rot_hi(x1.w, x2.w, c2.w, s2.w));
+    *reinterpret_cast<float4*>(row + d) = lo;
+    *reinterpret_cast<float4*>(row + d + half) = hi;
+    if (head >= n_q) {
+      uint16_t* dst = kc + (static_cast<int64_t>(pos) * n_kv + (head - n_q)) * hd;
+      *reinterpret_cast<uint2*>(dst + d) = half4(lo.x, lo.y, lo.z, lo.w);
+      *reinterpret_cast<uint2*>(dst + d + half) = half4(hi.x, hi.y, hi.z, hi.w);
+    }
+  } else {  // v: copy into the cache
+    uint16_t* dst = vc + (static_cast<int64_t>(pos) * n_kv + (head - n_q - n_kv)) * hd;
+    *reinterpret_cast<uint2*>(dst + d) = half4(x1.x, x1.y, x1.z, x1.w);
+    *reinterpret_cast<uint2*>(dst + d + half) = half4(x2.x, x2.y, x2.z, x2.w);
   }
 }
 
@@ -250,6 +314,13 @@ extern "C" int rope_kv_write(float* qkv, const float* cos_t, const float* sin_t,
                              int C, int n_q, int n_kv, int hd, int max_ctx, const int32_t* start, void* stream) {
   if (!qkv || !cos_t || !sin_t || !k_cache || !v_cache || !start) return Q4_ERR_NULL;
   if (C <= 0 || n_q <= 0 || n_kv <= 0 || hd <= 0 || hd % 2 || max_ctx <= 0) return Q4_ERR_SHAPE;
+  if (hd % 8 == 0 && aligned(qkv, 16) && aligned(cos_t, 16) && aligned(sin_t, 16) && aligned(k_cache, 8) &&
+      aligned(v_cache, 8)) {
+    const int64_t total = static_cast<int64_t>(C) * (n_q + 2 * n_kv) * (hd / 8);
+    hipLaunchKernelGGL(rope_kv4_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), qkv, cos_t, sin_t, k_cache, v_cache, C, n_q, n_kv, hd, max_ctx, start);
+    return launch_status();
+  }
   const int64_t total = static_cast<int64_t>(C) * (n_q + 2 * n_kv) * (hd / 2);
   hipLaunchKernelGGL(rope_kv_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, as_stream(stream),
                      qkv, cos_t, sin_t, k_cache, v_cache, C, n_q, n_kv, hd, max_ctx, start);

@@ -228,16 +228,20 @@ def test_rmsnorm_and_row_select(dev):
     assert torch.allclose(one[0], ref[3], rtol=2e-6, atol=1e-6)
 
 
-def test_rope_kv_write_bit_exact(dev):
-    nq, nkv, hd, Cn, start = 4, 2, 64, 6, 9
+@pytest.mark.parametrize("hd,start", [(64, 9), (128, 0), (6, 9), (64, 60)])
+def test_rope_kv_write_bit_exact(dev, hd, start):
+    """Both kernels (4 dims per thread for hd % 8 == 0, one pair per thread otherwise); rows whose
+    position is past max_ctx (start 60: positions 64, 65) are left as they are and write no cache row."""
+    nq, nkv, Cn = 4, 2, 6
     g = torch.Generator().manual_seed(8)
     qkv = torch.randn(Cn, (nq + 2 * nkv) * hd, generator=g)
     cos, sin = R.rope_tables(dict(hidden_size=256, num_attention_heads=nq, num_key_value_heads=nkv, head_dim=hd,
                                   rope_theta=10000.0, max_position_embeddings=64), 64)
-    pos = torch.arange(start, start + Cn)
-    q = qkv[:, : nq * hd].reshape(Cn, nq, hd)
-    k = qkv[:, nq * hd: (nq + nkv) * hd].reshape(Cn, nkv, hd)
-    v = qkv[:, (nq + nkv) * hd:].reshape(Cn, nkv, hd)
+    n_in = min(Cn, 64 - start)  # rows with a position inside the 64-row tables and caches
+    pos = torch.arange(start, start + n_in)
+    q = qkv[:n_in, : nq * hd].reshape(n_in, nq, hd)
+    k = qkv[:n_in, nq * hd: (nq + nkv) * hd].reshape(n_in, nkv, hd)
+    v = qkv[:n_in, (nq + nkv) * hd:].reshape(n_in, nkv, hd)
     cs, sn = cos[pos][:, None], sin[pos][:, None]
     q_ref = q * cs + R.rotate_half(q) * sn
     k_ref = k * cs + R.rotate_half(k) * sn
@@ -245,10 +249,12 @@ def test_rope_kv_write_bit_exact(dev):
     vc = torch.zeros(64, nkv, hd, dtype=torch.float16, device=dev)
     qd = qkv.to(dev)
     ops.rope_kv_write(qd, cos.to(dev), sin.to(dev), kc, vc, nq, nkv, hd, torch.tensor([start], dtype=torch.int32, device=dev))
-    assert torch.equal(qd.cpu()[:, : nq * hd].reshape(Cn, nq, hd), q_ref)
-    assert torch.equal(kc.cpu()[start:start + Cn], k_ref.half())
-    assert torch.equal(vc.cpu()[start:start + Cn], v.half())
-    assert kc.cpu()[:start].abs().sum() == 0 and kc.cpu()[start + Cn:].abs().sum() == 0
+    assert torch.equal(qd.cpu()[:n_in, : nq * hd].reshape(n_in, nq, hd), q_ref)
+    assert torch.equal(qd.cpu()[n_in:], qkv[n_in:])
+    assert torch.equal(kc.cpu()[start:start + n_in], k_ref.half())
+    assert torch.equal(vc.cpu()[start:start + n_in], v.half())
+    assert kc.cpu()[:start].abs().sum() == 0 and kc.cpu()[start + n_in:].abs().sum() == 0
+    assert vc.cpu()[:start].abs().sum() == 0 and vc.cpu()[start + n_in:].abs().sum() == 0
 
 
 def test_silu_mul(dev):
