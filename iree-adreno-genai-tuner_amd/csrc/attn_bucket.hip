@@ -257,10 +257,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 }
 
 // Merge the splits of each (row, head): o = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
-// One workgroup of HD threads per (row, head); only the splits holding keys <= pos are read. Every
-// load of the first kBatch splits is issued before any use (thread d holds split d's (m, l) and
-// its own dim of kBatch o partials), so the merge costs one memory round trip; the max and the
-// denominator are block reductions through LDS, the numerator is summed in ascending split order.
+// One workgroup of HD threads per (row, head); only the splits holding keys <= pos are used. The loads
+// that do not need the position are issued first: this thread's dim of the first kBatch splits' o
+// partials and (thread i) split i's (m, l), so the merge costs one memory round trip, overlapped with
+// the read of the position; splits past it are then masked by selection (their workspace entries may
+// hold anything). The max and the denominator are block reductions through LDS, the numerator is
+// summed in ascending split order.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
                                                          float* __restrict__ out, int n_q, int n_splits, int S,
@@ -272,14 +274,16 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   __shared__ float red[NW];
   const int c = blockIdx.x / n_q, h = blockIdx.x % n_q;
   const int d = threadIdx.x;
-  const int pos = start_p[0] + c;
-  const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos (n_splits <= 512: host)
   const size_t base = (static_cast<size_t>(c) * n_q + h) * n_splits;
   float ov[kBatch];
 #pragma unroll
-  for (int j = 0; j < kBatch; ++j) ov[j] = j < ns ? ws_o[(base + j) * HD + d] : 0.0f;
-  float mloc = -INFINITY;
-  for (int i = d; i < ns; i += HD) mloc = fmaxf(mloc, ws_ml[2 * (base + i)]);
+  for (int j = 0; j < kBatch; ++j) ov[j] = j < n_splits ? ws_o[(base + j) * HD + d] : 0.0f;
+  float2 ml = make_float2(-INFINITY, 0.0f);
+  if (d < n_splits) ml = reinterpret_cast<const float2*>(ws_ml)[base + d];
+  const int pos = start_p[0] + c;
+  const int ns = min(n_splits, pos / S + 1);  // splits holding keys <= pos (n_splits <= 512: host)
+  float mloc = d < ns ? ml.x : -INFINITY;
+  for (int i = d + HD; i < ns; i += HD) mloc = fmaxf(mloc, ws_ml[2 * (base + i)]);
   const float mw = group_max<64>(mloc);
   if ((d & 63) == 0) red[d >> 6] = mw;
   __syncthreads();
@@ -287,7 +291,12 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* __restric
   for (int w = 1; w < NW; ++w) M = fmaxf(M, red[w]);
   __syncthreads();
   float den = 0.0f;
-  for (int i = d; i < ns; i += HD) {
+  if (d < ns) {
+    const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - M);
+    wts[d] = w;
+    den = fmaf(w, ml.y, den);
+  }
+  for (int i = d + HD; i < ns; i += HD) {
     const float m = ws_ml[2 * (base + i)];
     const float w = m == -INFINITY ? 0.0f : expf(m - M);
     wts[i] = w;
