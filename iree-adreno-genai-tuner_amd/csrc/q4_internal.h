@@ -13,6 +13,11 @@ namespace q4 {
 // q4_linear_ws's GEMM on given planes (power-of-two group).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st);
+// The gate/up projection with silu(gate) * up written as the [M, N / 2] planes oh / ol (ol = oh + M N / 2)
+// of the down projection; Q4_ERR_UNSUPPORTED when the shape does not take the fused tile (the caller then
+// runs q4_linear_planes + silu_mul_planes).
+int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
+                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st);
 // rmsnorm_f32 of M rows (no row selection), written as planes.
 int rmsnorm_planes(const float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
                    hipStream_t st);

@@ -337,11 +337,35 @@ struct LinWsCfg {
   static_assert(kRed <= static_cast<size_t>(NST) * kStage, "k-split reduction fits in the stages");
 };
 
-template <int BM, int BN, int WM, int WN, int NST, int KS>
+// silu(g) * u rounded like the separate tensor ops (llama_q4.py:236), as in the element-wise kernels.
+__device__ __forceinline__ float silu_mul_exact(float g, float u) {
+#pragma clang fp contract(off)
+  const float e = expf(-g);
+  const float den = 1.0f + e;
+  const float sg = g / den;
+  return sg * u;
+}
+
+// EPI = 1 (SwiGLU): the N columns are the fused [gate | up] weight's 2 I rows, taken in 32-column blocks
+// alternately from gate and up (block B <- rows (B & 1) I + 32 (B >> 1) + [0, 32)), so the two tiles of
+// a wave hold the gate and up values of the same 32 outputs in the same lanes; the epilogue writes
+// silu(gate) * up for [M, I] into the fp16 (hi, lo) planes at Y (hi) and Y + M I (lo), the input of the
+// down projection. R must be null.
+template <int BM, int BN, int WM, int WN, int NST, int KS, int EPI = 0>
 __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
     const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n) {
   using G = LinWsCfg<BM, BN, WM, WN, NST, KS>;
+  static_assert(EPI == 0 || (G::TN % 2 == 0 && G::WTN % 64 == 0 && BN % 64 == 0), "SwiGLU pairs tiles 2j, 2j + 1");
+  // weight row of virtual column v
+  auto phys = [&](int v) -> int {
+    if constexpr (EPI == 0) {
+      return v;
+    } else {
+      const int blk = v >> 5;
+      return (blk & 1) * (N >> 1) + ((blk >> 1) << 5) + (v & 31);
+    }
+  };
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
@@ -384,7 +408,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const int b = wave + j * G::kWaves;
     const int r = 32 * b + (lane >> 1);
     wreal[j] = b < BN / 32;
-    woff[j] = wreal[j] && n0 + r < N ? static_cast<uint32_t>(n0 + r) * (K / 2) + (lane & 1) * 16u : kOOBw;
+    woff[j] = wreal[j] && n0 + r < N ? static_cast<uint32_t>(phys(n0 + r)) * (K / 2) + (lane & 1) * 16u : kOOBw;
   }
   unsigned char* junk = lds + NST * G::kStage;
   // Every step issues the same loads (steps past K load zeros into a free stage), so the number of
@@ -418,7 +442,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
       const bool real = i < 2 * G::kSBlk;
       const int slot = i / G::kSBlk, blk = i - slot * G::kSBlk;
       const int col = n0 + blk * 64 + lane;
-      const uint32_t e = static_cast<uint32_t>(col) * spr + (slot ? g1 : g0);
+      const uint32_t e = static_cast<uint32_t>(phys(col)) * spr + (slot ? g1 : g0);
       load_lds4(sr, real ? ss + (slot * G::kSBlk + blk) * 256 : junk,
                 real && kin && col < N ? (e >> 1) * 4u : kOOBw);
     }
@@ -426,7 +450,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
 
   auto scale_elem = [&](int j, int g) -> uint32_t {
     const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
-    return static_cast<uint32_t>(col) * spr + g;
+    return static_cast<uint32_t>(phys(col)) * spr + g;
   };
   // scale of group g for this lane's column in tile column j, from slot `slot` of the stage at ss
   auto scale_of = [&](const unsigned char* ss, int slot, int j, int g) {
@@ -550,6 +574,24 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
           for (int e = 0; e < 16; ++e) acc[i][j][e] += *slot(g2, i, j, e);
   }
 
+  if constexpr (EPI == 1) {
+    const int I = N >> 1;
+    uint16_t* oh = reinterpret_cast<uint16_t*>(Y);
+    uint16_t* ol = oh + static_cast<int64_t>(M) * I;
+#pragma unroll
+    for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::TN; j += 2)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+          const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);  // the gate column; col + 32 is up
+          if (row < M && col < N)
+            store_x_planes(oh, ol, static_cast<int64_t>(row) * I + phys(col),
+                           silu_mul_exact(acc[i][j][e], acc[i][j + 1][e]));
+        }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < G::TM; ++i)
 #pragma unroll
@@ -665,6 +707,30 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   }
   hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
                      (int)M, (int)N, (int)K, group, tiles_n);
+  return launch_status();
+}
+
+// The gate/up projection with the SwiGLU epilogue (EPI = 1) on the tile the fixed rule picks for it at
+// M <= 256 (64x256, one workgroup per CU); other shapes return Q4_ERR_UNSUPPORTED and the caller runs
+// q4_linear_planes + silu_mul_planes. oh / ol: the [M, N / 2] output planes (must not alias xh / xl).
+int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
+                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st) {
+  const char* ov = getenv("Q4_LINEAR_CFG");
+  if ((ov && *ov) || getenv("Q4_SWIGLU_UNFUSED")) return Q4_ERR_UNSUPPORTED;
+  if (group & (group - 1)) return Q4_ERR_UNSUPPORTED;
+  constexpr LinWsTile t = kLinWsTiles[12];
+  const int64_t wide = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+  if (!(M <= 256 && wide >= 256) || N % t.bn || (N / 2) % 32 || ol != oh + M * (N / 2)) return Q4_ERR_UNSUPPORTED;
+  auto fn = q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, 1>;
+  constexpr size_t lds = LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
+  if (lds > 64 * 1024) {
+    Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(lds)));
+  }
+  const int tiles_n = static_cast<int>(N / t.bn);
+  const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
+  hipLaunchKernelGGL(fn, dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), lds, st, xh, xl, qw, sc,
+                     reinterpret_cast<float*>(oh), nullptr, (int)M, (int)N, (int)K, group, tiles_n);
   return launch_status();
 }
 

@@ -187,9 +187,19 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
       Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
     } else if (planes) {
       Q4_TRY(q4::rmsnorm_planes(h, ly.ln_post, xh, xl, C, D, m->eps, st));
-      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st));
-      Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
-      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
+      // gate/up + SwiGLU in one kernel where the shape takes it (its planes go to the gu buffer, which
+      // holds the [C, 2 inter] fp32 otherwise), else the GEMM and silu_mul as two kernels
+      uint16_t* ah = reinterpret_cast<uint16_t*>(gu);
+      uint16_t* al = ah + static_cast<int64_t>(C) * m->inter;
+      const int fused = q4::q4_linear_planes_swiglu(xh, xl, C, ly.wgu_q, ly.wgu_s, ah, al, 2 * m->inter, D, m->group, st);
+      if (fused == Q4_OK) {
+        Q4_TRY(q4::q4_linear_planes(ah, al, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
+      } else {
+        if (fused != Q4_ERR_UNSUPPORTED) return fused;
+        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st));
+        Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
+        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
+      }
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, lin_ws, lo.lin_bytes, stream));

@@ -121,3 +121,26 @@ def test_llama32_3b_generation_matches_golden(dev):
     assert res["tokens"] == gold["tokens"]
     del model
     torch.cuda.empty_cache()
+
+
+def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch):
+    """A 256-row chunk with intermediate 8192 takes the gate/up GEMM with the SwiGLU epilogue (planes of
+    silu(gate) * up written by the GEMM): bit-identical logits and caches to the GEMM + silu_mul pair
+    (Q4_SWIGLU_UNFUSED), and the oracle's next token with logits within the per-op tolerance."""
+    cfg = dict(synth.TINY, intermediate_size=8192, num_hidden_layers=2)
+    ours, ref = build_pair(cfg, 32, 256)
+    prompt = synth.prompt_ids(256, cfg["vocab_size"], seed=3)
+    toks = torch.tensor([prompt], dtype=torch.int32)
+    start, last = torch.tensor([0], dtype=torch.int32), torch.tensor([255], dtype=torch.int32)
+    c_fused = ours.new_caches()
+    n_f, l_f = ours.step(toks, start, last, c_fused, 256)
+    monkeypatch.setenv("Q4_SWIGLU_UNFUSED", "1")
+    c_two = ours.new_caches()
+    n_t, l_t = ours.step(toks, start, last, c_two, 256)
+    monkeypatch.delenv("Q4_SWIGLU_UNFUSED")
+    assert torch.equal(l_f, l_t) and int(n_f.item()) == int(n_t.item())
+    for a, b in zip(c_fused, c_two):
+        assert torch.equal(a, b)
+    r_n, r_l = ref.step(toks, start, last, ref.new_caches(), 256)
+    assert int(n_f.item()) == int(r_n.item())
+    assert (l_f.cpu() - r_l).abs().max().item() <= tol(r_l)
