@@ -50,6 +50,8 @@ AttnPlan plan_for(int C, int n_q, int n_kv, int L) {
     p.mfma = true;
     p.CB = 32;
     p.S = L <= 256 ? 64 : 128;
+    const char* ov = getenv("Q4_ATTN_PS");  // sweep override: keys per split (a multiple of 32, <= 512)
+    if (ov && atoi(ov) >= 32 && atoi(ov) <= 512 && atoi(ov) % 32 == 0) p.S = atoi(ov);
   } else {
     p.CB = kMaxQ / g < C ? kMaxQ / g : C;
     p.S = 64;
