@@ -81,7 +81,9 @@ int q4_dequant(const int32_t* qweight, const uint16_t* scales, void* w, int w_dt
  * (llama_q4.py:69-72): y[n] = residual[n] + sum_k x[k] * (nib[n,k] - 8) * scale[n, k/group].
  * x: K elements of x_dtype; y: N elements of y_dtype; residual: NULL or N fp32 (only with
  * y_dtype == Q4_F32; may alias y). Accumulation is fp32.
- * Requires K % 8 == 0, K % group == 0, group % 8 == 0, K <= 16384, 16-byte aligned qweight/x. */
+ * Requires K % 8 == 0, K % group == 0, group % 8 == 0, K < 2^28, 4-byte aligned qweight/x and
+ * 2-byte aligned y. Shapes with K % 32 == 0, group = 32 * 2^j, K <= 16384 and 16-byte aligned
+ * qweight/x take the staged kernels; the rest take a one-wave-per-row generic kernel. */
 int q4_gemv(const int32_t* qweight, const uint16_t* scales, const void* x, int x_dtype, void* y,
             int y_dtype, const float* residual, int64_t N, int64_t K, int group, void* stream);
 

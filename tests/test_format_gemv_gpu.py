@@ -108,6 +108,45 @@ def test_gemv_f32_model_path(dev, n, k, group):
     assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
 
 
+@pytest.mark.parametrize("n,k,group", [(512, 16384, 128), (300, 16512, 128), (64, 18432, 96)])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_gemv_max_k(dev, n, k, group, xdt):
+    """K = 16384 is the largest K the staged (vectorised and matrix-core) kernels take; K = 16512 and a
+    non-power-of-two group go to the generic kernel. Both must agree with the oracle."""
+    g = torch.Generator().manual_seed(k + group)
+    w = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(w, group)
+    x = torch.randn(k, generator=g).to(xdt)
+    ref = R.dequantize_q4(qw, sc, group).double() @ x.double()
+    rms = ref.pow(2).mean().sqrt().item()
+    ydt = xdt
+    y = poison(torch.empty(n, dtype=ydt, device=dev))
+    ops.q4_gemv(qw.to(dev), sc.to(dev), x.to(dev), group, out=y)
+    tol = 1e-2 if xdt == torch.float16 else 1e-5
+    err = (y.cpu().double() - ref).abs().max().item()
+    assert err <= tol * rms, (err, rms)
+
+
+def test_gemv_4byte_aligned_operands(dev):
+    """qweight and x only 4-byte aligned (offset by one element): the generic kernel takes the call."""
+    n, k, group = 200, 3072, 128
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(n, k, generator=g) * 0.02
+    qw, sc = R.quantize_q4(w, group)
+    x = torch.randn(k, generator=g)
+    ref = R.dequantize_q4(qw, sc, group).double() @ x.double()
+    rms = ref.pow(2).mean().sqrt().item()
+    qbuf = torch.empty(n * k // 8 + 1, dtype=torch.int32, device=dev)
+    qbuf[1:] = qw.reshape(-1).to(dev)
+    xbuf = torch.empty(k + 1, dtype=torch.float32, device=dev)
+    xbuf[1:] = x.to(dev)
+    qd, xd = qbuf[1:].view(n, k // 8), xbuf[1:]
+    assert qd.data_ptr() % 16 and xd.data_ptr() % 16
+    y = poison(torch.empty(n, dtype=torch.float32, device=dev))
+    ops.q4_gemv(qd, sc.to(dev), xd, group, out=y)
+    assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+
+
 def test_gemv_all_configs_agree(dev):
     """Every entry of the explicit tile list computes the same GEMV (coverage of the tile table)."""
     from q4llm._lib import LIB
