@@ -137,10 +137,13 @@ def test_gemm_config3(dev, M, N, K):
     assert err <= 1e-2 * rms, (err, rms)
 
 
-@pytest.mark.parametrize("sid,M,N,K", [("S2", 128, 3072, 3072), ("S4", 16, 4096, 4096), ("S7", 1, 4096, 4096)])
+@pytest.mark.parametrize("sid,M,N,K", [("S1", 1024, 1024, 1024), ("S2", 128, 3072, 3072), ("S3", 4096, 64, 1024),
+                                        ("S4", 16, 4096, 4096), ("S5", 256, 256, 8192), ("S6", 2048, 2048, 32),
+                                        ("S7", 1, 4096, 4096), ("S8", 768, 768, 768)])
 def test_gemm_reference_nt_shapes_tol(dev, sid, M, N, K):
-    """The reference's NT shapes with its own data recipe and TOL (gemm/shapes.py:41-66):
-    U(-1,1) from default_rng(seed + id), max|C - Cref| / max|Cref| <= 5e-3."""
+    """All eight of the reference's problems with its own data recipe and TOL (gemm/shapes.py:41-66):
+    U(-1,1) from default_rng(seed + id), max|C - Cref| / max|Cref| <= 5e-3. The kernel is NT; the NN,
+    TN and TT problems (S1, S3, S5, S6, S8) run on their logical A [M,K] and B^T [N,K]."""
     rng = np.random.default_rng(0 + int(sid[1:]))
     a = rng.uniform(-1, 1, (M, K)).astype(np.float16)
     b = rng.uniform(-1, 1, (K, N)).astype(np.float16)
