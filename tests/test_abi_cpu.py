@@ -38,6 +38,9 @@ def test_status_strings():
     ((FAKE, FAKE, FAKE, 7, FAKE, 0, None, 8, 64, 32, None), "DTYPE"),
     ((FAKE, FAKE, FAKE, 0, FAKE, 1, FAKE, 8, 64, 32, None), "DTYPE"),       # residual with fp16 y
     ((FAKE + 1, FAKE, FAKE, 0, FAKE, 0, None, 8, 64, 32, None), "ALIGN"),
+    ((FAKE, FAKE, FAKE + 2, 1, FAKE, 1, None, 8, 64, 32, None), "ALIGN"),   # fp16 x only 2-byte aligned
+    ((FAKE, FAKE, FAKE, 1, FAKE + 1, 1, None, 8, 64, 32, None), "ALIGN"),   # fp16 y odd address
+    ((FAKE, FAKE, FAKE, 0, FAKE, 0, None, 8, 1 << 28, 32, None), "SHAPE"),  # K beyond 2^28 - 1
 ])
 def test_gemv_validation(args, code):
     assert LIB.raw("q4_gemv")(*args) == ERR[code]
