@@ -238,6 +238,11 @@ int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t
                const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* start[0] += delta on the device, stream ordered: the decode loop's position step (pos += 1,
+ * runner/llm_runner.c:233-245) for a loop that feeds the next token and position back on the
+ * device; one kernel, so it can be captured with q4llm_step into one graph. */
+int q4llm_advance_position(int32_t* start, int delta, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Measurement and tuning hooks (counterparts of gemm/roofline.py:27-70 and of the tuner's
  * candidate timing, scripts/tune/kernel_tuner.py:144-227; not part of the model path)

@@ -378,3 +378,18 @@ extern "C" int argmax_f32(const float* logits, int64_t V, int32_t* out, void* wo
   hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, static_cast<const Best*>(workspace), nb, out);
   return launch_status();
 }
+
+namespace q4 {
+namespace {
+__global__ void advance_position_kernel(int32_t* __restrict__ start, int delta) {
+  if (threadIdx.x == 0) start[0] += delta;
+}
+}  // namespace
+}  // namespace q4
+
+extern "C" int q4llm_advance_position(int32_t* start, int delta, void* stream) {
+  if (!start) return Q4_ERR_NULL;
+  if (!aligned(start, 4)) return Q4_ERR_ALIGN;
+  hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, as_stream(stream), start, delta);
+  return launch_status();
+}

@@ -257,13 +257,12 @@ void* need(Packed& pk, const std::string& name) {
 
 // Decode entry points (C == 1) feed themselves: their token buffer is their `next` buffer (q4llm_step
 // reads the tokens in its first kernel and writes next in its last) and the graph ends by adding 1
-// to start, so after a call the device inputs already hold what the following decode call passes;
-// `call` then skips the host-to-device copy.
-__global__ void advance_start_kernel(int32_t* start) { start[0] += 1; }
-
+// to start (q4llm_advance_position), so after a call the device inputs already hold what the
+// following decode call passes; `call` then skips the host-to-device copy.
 struct EntryPoint {
   int C = 0, L = 0;
-  int32_t *tokens = nullptr, *start = nullptr, *last = nullptr, *next = nullptr;  // device
+  int32_t* io = nullptr;  // device allocation [C + 3] int32 holding the four buffers below
+  int32_t *tokens = nullptr, *start = nullptr, *last = nullptr, *next = nullptr;  // device, inside io
   void* ws = nullptr;
   size_t ws_bytes = 0;
   hipGraphExec_t exec = nullptr;
@@ -292,24 +291,28 @@ struct Runner {
     EntryPoint e;
     e.C = C;
     e.L = L;
-    HIP_OK(hipMalloc(&e.tokens, sizeof(int32_t) * (C + 3)));
-    HIP_OK(hipMemset(e.tokens, 0, sizeof(int32_t) * (C + 3)));
-    e.start = e.tokens + C;
+    HIP_OK(hipMalloc(&e.io, sizeof(int32_t) * (C + 3)));
+    HIP_OK(hipMemset(e.io, 0, sizeof(int32_t) * (C + 3)));
+    e.tokens = e.io;
+    e.start = e.io + C;
     e.last = e.start + 1;
     e.next = e.last + 1;
     if (C == 1) e.tokens = e.next;
     Q4_OK_OR_DIE(q4llm_step_workspace_bytes(&model, C, L, &e.ws_bytes));
     HIP_OK(hipMalloc(&e.ws, e.ws_bytes));
     HIP_OK(hipMemset(e.ws, 0, e.ws_bytes));
-    raw_step(e);  // first launch outside capture: code objects and LDS attributes are set up here
+    // First launch outside capture (code objects and LDS attributes are set up here), at position
+    // max_ctx: the RoPE/KV-write kernels write no cache row there, so an entry point first built
+    // after the prompt is in the caches (no warm-up) leaves that prompt's K/V rows intact.
+    const int32_t setup_pos = model.max_ctx;
+    HIP_OK(hipMemcpy(e.start, &setup_pos, sizeof(int32_t), hipMemcpyHostToDevice));
+    raw_step(e);
     HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipMemset(e.io, 0, sizeof(int32_t) * (C + 3)));
     hipGraph_t g = nullptr;
     HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     raw_step(e);
-    if (C == 1) {
-      hipLaunchKernelGGL(advance_start_kernel, dim3(1), dim3(1), 0, stream, e.start);
-      HIP_OK(hipGetLastError());
-    }
+    if (C == 1) Q4_OK_OR_DIE(q4llm_advance_position(e.start, 1, stream));
     HIP_OK(hipStreamEndCapture(stream, &g));
     HIP_OK(hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0));
     HIP_OK(hipGraphDestroy(g));
@@ -510,7 +513,7 @@ int main(int argc, char** argv) {
   for (auto& kv : r.eps) {
     HIP_OK(hipGraphExecDestroy(kv.second.exec));
     HIP_OK(hipFree(kv.second.ws));
-    HIP_OK(hipFree(kv.second.tokens));
+    HIP_OK(hipFree(kv.second.io));
   }
   for (void* c : r.caches) HIP_OK(hipFree(c));
   for (void* d : pk.device_buffers) HIP_OK(hipFree(d));

@@ -680,6 +680,21 @@ int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_
 
 int q4_linear_ws_num_tiles() { return kNumLinWs; }
 
+namespace {
+// What the pipelined GEMM's index arithmetic assumes: every 64-k stage lies in whole groups of a
+// power of two >= 32 (at most two scale slots per stage, groups found by shifts), K a multiple of
+// 64, and 32-bit element offsets.
+int planes_args(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc, int64_t N,
+                int64_t K, int group) {
+  if (!xh || !xl || !qw || !sc) return Q4_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0 || group < 32 || (group & (group - 1)) || K % 64 || K % group) return Q4_ERR_SHAPE;
+  if (M * K * 4 >= (int64_t{1} << 31) || N * (K / 2) >= (int64_t{1} << 31) || M > INT32_MAX || N > INT32_MAX)
+    return Q4_ERR_SHAPE;
+  if (!aligned(xh, 16) || !aligned(xl, 16) || !aligned(qw, 16)) return Q4_ERR_ALIGN;
+  return Q4_OK;
+}
+}  // namespace
+
 // The pipelined GEMM on x given as fp16 (hi, lo) planes (store_x_planes layout, [M, K] each);
 // power-of-two groups only. Tile rule from a sweep of every entry over the 3B prefill shapes at
 // M = 128, 256 and 1024 (graph replays on one MI355X): the 32x64 k-split tile while it gives at most
@@ -687,6 +702,8 @@ int q4_linear_ws_num_tiles() { return kNumLinWs; }
 // Q4_LINEAR_CFG overrides.
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st) {
+  if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
+  if (!y) return Q4_ERR_NULL;
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
@@ -715,9 +732,10 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
 // q4_linear_planes + silu_mul_planes. oh / ol: the [M, N / 2] output planes (must not alias xh / xl).
 int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                             uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st) {
+  if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
+  if (!oh || !ol) return Q4_ERR_NULL;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if ((ov && *ov) || getenv("Q4_SWIGLU_UNFUSED")) return Q4_ERR_UNSUPPORTED;
-  if (group & (group - 1)) return Q4_ERR_UNSUPPORTED;
   constexpr LinWsTile t = kLinWsTiles[12];
   const int64_t wide = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (!(M <= 256 && wide >= 256) || N % t.bn || (N / 2) % 32 || ol != oh + M * (N / 2)) return Q4_ERR_UNSUPPORTED;

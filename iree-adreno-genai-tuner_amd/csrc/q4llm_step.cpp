@@ -33,6 +33,10 @@ struct Layout {
 
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Shapes the matrix-core prefill GEMM takes: K % 64 == 0 and group % 32 == 0 (its stages hold 64 k
+// and at most two scale groups).
+bool linear_fits(int K, int group) { return K % 64 == 0 && group % 32 == 0 && K % group == 0; }
+
 int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   const size_t f = sizeof(float);
   const int nq = m->n_heads * m->head_dim, nkv = m->n_kv * m->head_dim;
@@ -56,10 +60,11 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   // prefill projections: the fp16 hi/lo planes of their input (largest K of the four)
   size_t lin = 0;
   if (C > 1) {
-    int64_t kmax = m->dim;
-    if (nq > kmax) kmax = nq;
-    if (m->inter > kmax) kmax = m->inter;
-    if (int st = q4_linear_workspace_bytes(C, kmax, &lin)) return st;
+    int64_t kmax = 0;
+    for (int k : {m->dim, nq, m->inter})
+      if (linear_fits(k, m->group) && k > kmax) kmax = k;
+    if (kmax > 0)
+      if (int st = q4_linear_workspace_bytes(C, kmax, &lin)) return st;
   }
   lo->lin = take(lin);
   lo->lin_bytes = lin;
@@ -83,10 +88,18 @@ int check_model(const q4llm_model* m) {
 }
 
 // y = residual + x W^T for C rows (C == 1: GEMV, else the fused int4 GEMM with its x planes in ws).
+// A prefill projection whose K or group the GEMM does not take (group 8 or 16, K % 64 != 0: legal
+// in the reference, llama_q4.py:31) runs one GEMV per row, each with the same fp32 arithmetic.
 int proj(int C, const float* x, const int32_t* q, const uint16_t* s, float* y, const float* res, int N, int K, int group,
          void* ws, size_t ws_bytes, void* stream) {
   if (C == 1) return q4_gemv(q, s, x, Q4_F32, y, Q4_F32, res, N, K, group, stream);
-  return q4_linear_ws(x, C, q, s, y, res, N, K, group, ws, ws_bytes, stream);
+  if (linear_fits(K, group)) return q4_linear_ws(x, C, q, s, y, res, N, K, group, ws, ws_bytes, stream);
+  for (int r = 0; r < C; ++r) {
+    const int64_t xo = static_cast<int64_t>(r) * K, yo = static_cast<int64_t>(r) * N;
+    if (int st = q4_gemv(q, s, x + xo, Q4_F32, y + yo, Q4_F32, res ? res + yo : nullptr, N, K, group, stream))
+      return st;
+  }
+  return Q4_OK;
 }
 
 // The fused decode GEMVs (qkv and gate/up, K = dim) need the vectorised layout: K % 32 == 0,
@@ -151,7 +164,8 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   // Prefill with a power-of-two group: the norms, the attention merge and SwiGLU write their results
   // straight as the fp16 (hi, lo) planes the following projection reads (in the lin workspace).
   const int kmax = std::max(D, std::max(nq_w, m->inter));
-  const bool planes = C > 1 && (m->group & (m->group - 1)) == 0 && D % 8 == 0 && nq_w % 8 == 0 && m->inter % 8 == 0;
+  const bool planes = C > 1 && (m->group & (m->group - 1)) == 0 && linear_fits(D, m->group) &&
+                      linear_fits(nq_w, m->group) && linear_fits(m->inter, m->group);
   uint16_t* xh = static_cast<uint16_t*>(lin_ws);
   uint16_t* xl = xh + static_cast<size_t>(C) * kmax;
   const hipStream_t st = static_cast<hipStream_t>(stream);

@@ -371,15 +371,22 @@ class _StepGraph:
         model.workspace(Cn, L)  # allocate before capture
         s = torch.cuda.Stream(dev)
         s.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(s):  # warm-up launch (code objects, LDS attributes) outside capture
+        # Set-up launch outside capture (code objects, LDS attributes). It runs at position max_ctx,
+        # where the RoPE/KV-write kernels write no cache row, so caches holding a live sequence
+        # (an entry point built mid-generation, or a run without warm-up) are left untouched.
+        self.start.fill_(model.max_ctx)
+        with torch.cuda.stream(s):
             model._raw_step(self.tokens, Cn, self.start, self.last, self.cache_arr, L, self.next, self.logits)
         torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        self.start.zero_()
+        self.next.zero_()
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=s):
             model._raw_step(self.tokens, Cn, self.start, self.last, self.cache_arr, L, self.next, self.logits)
             if self.feeds_back:
-                self.start.add_(1)
+                LIB.call("q4llm_advance_position", ptr(self.start), 1, stream_of(dev))
 
     def set_inputs(self, tokens, start, last):
         self.tokens.copy_(torch.as_tensor(tokens, dtype=torch.int32).reshape(-1), non_blocking=False)

@@ -1,8 +1,10 @@
 """Tensor-level wrappers over the C ABI (include/q4llm.h).
 
 Each wrapper takes torch tensors that live on the ROCm device, allocates its outputs with torch,
-and calls one extern "C" entry point on torch's current stream. Shapes and dtypes are checked
-here; the library re-validates everything on its side.
+and calls one extern "C" entry point on torch's current stream. dtype, shape and contiguity of every
+tensor the library reads or writes through a raw pointer are checked here (ValueError) before the
+device is touched, because the library sees only pointers and sizes; it re-validates sizes and
+alignment on its side.
 """
 
 import ctypes as C
@@ -18,6 +20,33 @@ def _dev(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
             raise ValueError("q4llm ops take ROCm device tensors (torch 'cuda' device); got a CPU tensor")
+
+
+def _need(t, name, dtype, shape=None, contiguous=True):
+    """Raise ValueError unless t has `dtype`, `shape` (a tuple; None entries match anything) and is
+    contiguous."""
+    if t is None:
+        return
+    dts = dtype if isinstance(dtype, tuple) else (dtype,)
+    if t.dtype not in dts:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {' or '.join(map(str, dts))}")
+    if shape is not None and (t.dim() != len(shape) or any(w is not None and w != h for w, h in zip(shape, t.shape))):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+
+
+def _weights(qweight, scales, group):
+    """Check an int4 weight pair and return (N, K)."""
+    if qweight.dim() != 2:
+        raise ValueError(f"qweight: expected [N, K/8], got shape {tuple(qweight.shape)}")
+    n, kw = qweight.shape
+    k = kw * 8
+    if group <= 0 or k % group:
+        raise ValueError(f"group {group} does not divide K = {k}")
+    _need(qweight, "qweight", torch.int32, (n, kw))
+    _need(scales, "scales", torch.float16, (n, k // group))
+    return n, k
 
 
 def quantize_q4(w: torch.Tensor, group: int):
@@ -42,6 +71,7 @@ def unpack_q4(qweight: torch.Tensor) -> torch.Tensor:
 
 def dequantize_q4(qweight, scales, group, dtype=torch.float32):
     """(nibble - 8) * scale as [N, K] of `dtype`; llama_q4.py:48-51."""
+    _weights(qweight, scales, group)
     _dev(qweight, scales)
     n, kw = qweight.shape
     out = torch.empty(n, kw * 8, dtype=dtype, device=qweight.device)
@@ -52,13 +82,18 @@ def dequantize_q4(qweight, scales, group, dtype=torch.float32):
 
 def q4_gemv(qweight, scales, x, group, out_dtype=torch.float32, residual=None, out=None):
     """y [N] = residual + W x for one row x [K] (fp32 or fp16); QLinear._gemv_fused semantics."""
-    _dev(qweight, scales, x, residual)
-    n, kw = qweight.shape
+    n, k = _weights(qweight, scales, group)
     x = x.reshape(-1).contiguous()
+    _need(x, "x", (torch.float32, torch.float16), (k,))
+    _need(residual, "residual", torch.float32, (n,))
+    _need(out, "out", (torch.float32, torch.float16), (n,))
+    if residual is not None and out is not None and out.dtype != torch.float32:
+        raise ValueError("a residual needs an fp32 output")
+    _dev(qweight, scales, x, residual, out)
     if out is None:
         out = torch.empty(n, dtype=out_dtype, device=x.device)
     LIB.call("q4_gemv", ptr(qweight), ptr(scales), ptr(x), _DT[x.dtype], ptr(out), _DT[out.dtype],
-             ptr(residual), n, kw * 8, group, stream_of(x.device))
+             ptr(residual), n, k, group, stream_of(x.device))
     return out
 
 
@@ -113,10 +148,13 @@ def q4_gemv_cfg(qweight, scales, x, group, out, cfg=-1, grid=0):
 
 def q4_linear(x, qweight, scales, group, residual=None, out=None):
     """y [M, N] = residual + x [M, K] @ dequant(W)^T in fp32 (QLinear.forward at M > 1)."""
-    _dev(qweight, scales, x, residual)
-    m, k = x.shape
-    n = qweight.shape[0]
+    n, k = _weights(qweight, scales, group)
     x = x.contiguous()
+    _need(x, "x", torch.float32, (None, k))
+    m = x.shape[0]
+    _need(residual, "residual", torch.float32, (m, n))
+    _need(out, "out", torch.float32, (m, n))
+    _dev(qweight, scales, x, residual, out)
     if out is None:
         out = torch.empty(m, n, dtype=torch.float32, device=x.device)
     LIB.call("q4_linear", ptr(x), m, ptr(qweight), ptr(scales), ptr(out), ptr(residual), n, k, group,
@@ -126,10 +164,14 @@ def q4_linear(x, qweight, scales, group, residual=None, out=None):
 
 def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=None):
     """q4_linear through the workspace entry point (x split once, multi-stage MFMA pipeline)."""
-    _dev(qweight, scales, x, residual)
-    m, k = x.shape
-    n = qweight.shape[0]
+    n, k = _weights(qweight, scales, group)
     x = x.contiguous()
+    _need(x, "x", torch.float32, (None, k))
+    m = x.shape[0]
+    _need(residual, "residual", torch.float32, (m, n))
+    _need(out, "out", torch.float32, (m, n))
+    _need(workspace, "workspace", torch.uint8, None)
+    _dev(qweight, scales, x, residual, out, workspace)
     if out is None:
         out = torch.empty(m, n, dtype=torch.float32, device=x.device)
     b = C.c_size_t(0)
@@ -143,9 +185,15 @@ def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=N
 
 def gemm_f16_nt(a, b, out=None):
     """C [M, N] fp16 = A [M, K] @ B [N, K]^T with fp32 accumulation (gemm/shapes.py 'NT')."""
-    _dev(a, b)
     m, k = a.shape
     n = b.shape[0]
+    _need(a, "A", torch.float16, (m, k), contiguous=False)
+    _need(b, "B", torch.float16, (n, k), contiguous=False)
+    _need(out, "C", torch.float16, (m, n), contiguous=False)
+    for t, nm in ((a, "A"), (b, "B"), (out, "C")):
+        if t is not None and t.stride(1) != 1:
+            raise ValueError(f"{nm}: rows must be contiguous (stride(1) == 1)")
+    _dev(a, b, out)
     if out is None:
         out = torch.empty(m, n, dtype=torch.float16, device=a.device)
     LIB.call("gemm_f16_nt", ptr(a), ptr(b), ptr(out), m, n, k, a.stride(0), b.stride(0), out.stride(0),

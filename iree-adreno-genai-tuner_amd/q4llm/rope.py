@@ -2,7 +2,7 @@
 
 The reference takes its tables from transformers' LlamaRotaryEmbedding. They are computed here
 without transformers, with the same fp32 tensor expressions (default RoPE and the Llama-3 frequency
-scaling), so the tables are bit-identical (tests/test_rope.py checks this against transformers
+scaling), so the tables are bit-identical (tests/test_rope_runner_cpu.py checks this against transformers
 when it is installed). They are load-time host tables shared by every step; the GPU only gathers
 rows of them.
 """

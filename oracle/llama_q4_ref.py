@@ -137,6 +137,22 @@ def pad_to(n: int, m: int) -> int:
     return (n + m - 1) // m * m
 
 
+def attention(q, kc, vc, allowed, L, scale):
+    """The attention block of llama_q4.py:224-232: q [C, nh, hd] fp32 (RoPE applied), caches
+    [>= L, nkv, hd], allowed [C, L] bool (key_pos <= pos); scores masked with -1e30, fp32 softmax,
+    bmm with the values. Returns o [C, nh * hd] fp32."""
+    C, nh, hd = q.shape
+    nkv = kc.shape[1]
+    g = nh // nkv
+    keys = kc[:L].float().permute(1, 2, 0)                              # [kv, hd, L]
+    vals = vc[:L].float().permute(1, 0, 2)                              # [kv, L, hd]
+    qg = q.reshape(C, nkv, g, hd).permute(1, 2, 0, 3).reshape(nkv, g * C, hd)
+    s = (torch.bmm(qg, keys) * scale).reshape(nkv, g, C, L)
+    s = torch.where(allowed[None, None], s, torch.full_like(s, -1e30))
+    p = torch.softmax(s, dim=-1).reshape(nkv, g * C, L)
+    return torch.bmm(p, vals).reshape(nkv, g, C, hd).permute(2, 0, 1, 3).reshape(C, nh * hd)
+
+
 class LlamaQ4Ref:
     """LlamaQ4 (llama_q4.py:158-243) on the CPU, built from an HF-style state dict `sd` and an HF
     config dict `cfg` (tied embeddings). Intermediate is padded to a multiple of `group` (module
@@ -176,6 +192,31 @@ class LlamaQ4Ref:
         self.ln_f = sd["model.norm.weight"].float()
         self.cos, self.sin = rope if rope is not None else rope_tables(cfg, max_ctx)
 
+    @classmethod
+    def from_quantized(cls, pc, t, cache=False, vocab_chunk=32064):
+        """A model over already-quantized weights: `pc` the packed config (dim, n_layers, n_heads, n_kv,
+        head_dim, inter, vocab, group, max_ctx, eps) and `t` CPU tensors named as the packed-weight file
+        (embed.qweight / .scales, layers.{i}.{wqkv,wo,wgu,wdown}.qweight / .scales, layers.{i}.ln_in /
+        .ln_post, ln_f, cos, sin). cache=False re-dequantizes every weight on every call, the
+        reference's eager QLinear.forward (llama_q4.py:72)."""
+        self = cls.__new__(cls)
+        self.cfg = None
+        self.n_layers, self.dim, self.n_heads, self.n_kv = pc["n_layers"], pc["dim"], pc["n_heads"], pc["n_kv"]
+        self.head_dim, self.inter, self.eps = pc["head_dim"], pc["inter"], pc["eps"]
+        self.max_ctx, self.group = pc["max_ctx"], pc["group"]
+        g = self.group
+        self.embed = QEmbeddingRef(group=g, chunk_rows=vocab_chunk, qweight=t["embed.qweight"],
+                                   scales=t["embed.scales"], cache=cache)
+        self.layers = []
+        for i in range(self.n_layers):
+            ly = {nm: QLinearRef(group=g, qweight=t[f"layers.{i}.{nm}.qweight"], scales=t[f"layers.{i}.{nm}.scales"],
+                                 cache=cache) for nm in ("wqkv", "wo", "wgu", "wdown")}
+            ly["ln_in"], ly["ln_post"] = t[f"layers.{i}.ln_in"].float(), t[f"layers.{i}.ln_post"].float()
+            self.layers.append(ly)
+        self.ln_f = t["ln_f"].float()
+        self.cos, self.sin = t["cos"].float(), t["sin"].float()
+        return self
+
     def new_caches(self, dtype=torch.float16):
         """llama_q4.py:241-243: 2 * n_layers zeroed [max_ctx, n_kv, head_dim] caches."""
         return [torch.zeros(self.max_ctx, self.n_kv, self.head_dim, dtype=dtype) for _ in range(2 * self.n_layers)]
@@ -191,7 +232,6 @@ class LlamaQ4Ref:
         sin = self.sin.index_select(0, pos).unsqueeze(1)
         allowed = torch.arange(L)[None, :] <= pos[:, None]                    # [C, L]
         nh, nkv, hd = self.n_heads, self.n_kv, self.head_dim
-        g = nh // nkv
         scale = 1.0 / math.sqrt(hd)
         for i, ly in enumerate(self.layers):
             kc, vc = caches[2 * i], caches[2 * i + 1]
@@ -203,13 +243,7 @@ class LlamaQ4Ref:
             k = k * cos + rotate_half(k) * sin
             kc.index_copy_(0, pos, k.to(kc.dtype))
             vc.index_copy_(0, pos, v.to(vc.dtype))
-            keys = kc[:L].float().permute(1, 2, 0)                              # [kv, hd, L]
-            vals = vc[:L].float().permute(1, 0, 2)                              # [kv, L, hd]
-            qg = q.reshape(C, nkv, g, hd).permute(1, 2, 0, 3).reshape(nkv, g * C, hd)
-            s = (torch.bmm(qg, keys) * scale).reshape(nkv, g, C, L)
-            s = torch.where(allowed[None, None], s, torch.full_like(s, -1e30))
-            p = torch.softmax(s, dim=-1).reshape(nkv, g * C, L)
-            o = torch.bmm(p, vals).reshape(nkv, g, C, hd).permute(2, 0, 1, 3).reshape(C, nh * hd)
+            o = attention(q, kc, vc, allowed, L, scale)
             h = h + ly["wo"](o)
             gu = ly["wgu"](rms_norm(h, ly["ln_post"], self.eps))
             h = h + ly["wdown"](F.silu(gu[:, : self.inter]) * gu[:, self.inter:])

@@ -144,3 +144,32 @@ def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch
     r_n, r_l = ref.step(toks, start, last, ref.new_caches(), 256)
     assert int(n_f.item()) == int(r_n.item())
     assert (l_f.cpu() - r_l).abs().max().item() <= tol(r_l)
+
+
+def test_group16_step_and_generation_vs_oracle(dev):
+    """group 16 (legal in the reference: group % 8 == 0, llama_q4.py:31): the matrix-core prefill GEMM
+    takes only groups of 32 * 2^j, so prefill runs one GEMV per row; decode takes the generic GEMV
+    path. Logits within the per-op tolerance and greedy tokens equal to the oracle's."""
+    ours, ref = build_pair(synth.TINY, 16, 128)
+    assert ours.inter == 688
+    prompt = synth.prompt_ids(16, 1024, seed=0)
+    toks = torch.tensor([prompt], dtype=torch.int32)
+    start, last = torch.tensor([0], dtype=torch.int32), torch.tensor([15], dtype=torch.int32)
+    n1, l1 = ours.step(toks, start, last, ours.new_caches(), 64)
+    r1, rl1 = ref.step(toks, start, last, ref.new_caches(), 64)
+    assert int(n1.item()) == int(r1.item())
+    assert (l1.cpu() - rl1).abs().max().item() <= tol(rl1)
+    want = R.generate(ref, prompt, 12, 8, [16, 32, 64])
+    assert llm_runner.run(ours, prompt, 12, 8, [16, 32, 64])["tokens"] == want
+
+
+def test_no_warmup_entry_points_built_mid_generation(dev):
+    """warm-up 0: each entry point is first built after earlier chunks (or the prompt) are in the
+    caches, including a prefill bucket switch (16 -> 32) and a decode bucket switch (32 -> 64).
+    Building an entry point must leave the live K/V rows intact, so the tokens equal the oracle's."""
+    model, ref = build_pair(synth.TINY, 32, 128)
+    prompt = synth.prompt_ids(21, 1024, seed=3)
+    want = R.generate(ref, prompt, 20, 8, [16, 32, 64])
+    res = llm_runner.run(model, prompt, 20, 8, [16, 32, 64], warmup=0)
+    assert sorted({L for L, _ in res["steps"]}) == [32, 64]
+    assert res["tokens"] == want

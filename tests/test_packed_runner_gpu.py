@@ -80,6 +80,17 @@ def test_native_runner_ragged_prompt_stop_ids_and_max_schedule(packed_file, tmp_
     assert res3["tokens"] == py["tokens"] and {L for L, _ in res3["steps"]} == {64}
 
 
+def test_native_runner_no_warmup_keeps_live_kv(packed_file, tmp_path):
+    """--warmup=0: each entry point (a prefill bucket switch 16 -> 32, a decode switch 32 -> 64) is
+    first built while the caches hold the live sequence; its set-up launch must not write them."""
+    p, model = packed_file
+    prompt = synth.prompt_ids(21, 1024, seed=3)
+    py = llm_runner.run(model, prompt, 20, 8, [16, 32, 64])
+    res = run_native(p, prompt, tmp_path, "--max_new_tokens=20", "--chunk=8", "--buckets=16,32,64", "--warmup=0")
+    assert {L for L, _ in res["steps"]} == {32, 64}
+    assert res["tokens"] == py["tokens"]
+
+
 def test_context_sweep_records(packed_file, tmp_path):
     """q4llm.sweep (scripts/llm/bench.py:69-107 contract): one record per (kind, ctx, schedule) with
     the runner's keys plus kind/ctx/tag, and the summary table over them."""
