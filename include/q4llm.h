@@ -238,6 +238,24 @@ int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t
                const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the per-GPU scratch array of q4llm_step_noalloc: 64 MiB. That covers every decode step
+ * (C == 1; the Llama-3.2-3B shape needs 1.03 MiB) and prefill chunks up to that size (3B shape:
+ * C = 256 at L <= 512 needs 58.7 MiB; q4llm_step_workspace_bytes gives the figure for a shape). */
+#define Q4LLM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* q4llm_step without a workspace argument and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The step's scratch is a file-scope device
+ * array of Q4LLM_NOALLOC_SCRATCH_BYTES, one per GPU, held until the process ends; its device
+ * address is looked up with hipGetSymbolAddress on the first call on each device (make that first
+ * call outside graph capture). Same arguments, kernels and results as q4llm_step; returns
+ * Q4_ERR_WORKSPACE when q4llm_step_workspace_bytes(m, C, L) exceeds Q4LLM_NOALLOC_SCRATCH_BYTES.
+ * Every call on one GPU shares that GPU's array (the last call's contents stay in it; nothing in it
+ * needs to start at zero): calls that overlap on one GPU, from two streams or two threads, race. */
+int q4llm_step_noalloc(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start,
+                       const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
+                       void* stream);
+
 /* start[0] += delta on the device, stream ordered: the decode loop's position step (pos += 1,
  * runner/llm_runner.c:233-245) for a loop that feeds the next token and position back on the
  * device; one kernel, so it can be captured with q4llm_step into one graph. */

@@ -20,7 +20,9 @@
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
+#include <mutex>
 
+#include "q4_common.h"
 #include "q4_internal.h"
 #include "q4llm.h"
 
@@ -231,4 +233,58 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   Q4_TRY(argmax_f32(lg, m->vocab, next, amax_ws, lo.amax_bytes, stream));
 #undef Q4_TRY
   return Q4_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// q4llm_step_noalloc: q4llm_step with its workspace in a file-scope device array
+// ------------------------------------------------------------------------------------------------
+
+// One array per GPU: each device that loads this library holds its own copy, at its own address,
+// until the process ends. In host code `scratch` names a host-side stand-in, never a device address:
+// the device address comes from hipGetSymbolAddress, once per device, and only that is used.
+__device__ __align__(256) unsigned char scratch[Q4LLM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// The device address of `scratch` on the device that runs `stream`, looked up on first use with
+// that device current.
+int scratch_address(void* stream, void** out) {
+  int dev = 0;
+  Q4_CHECK_HIP(hipStreamGetDevice(q4::as_stream(stream), &dev));
+  if (dev < 0 || dev >= kMaxDevices) return Q4_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    int cur = 0;
+    Q4_CHECK_HIP(hipGetDevice(&cur));
+    if (cur != dev) Q4_CHECK_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) Q4_CHECK_HIP(hipSetDevice(cur));
+    if (e != hipSuccess) return q4::hip_fail(e);
+    if (!p) return Q4_ERR_NULL;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return Q4_OK;
+}
+
+}  // namespace
+
+extern "C" int q4llm_step_noalloc(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start,
+                                  const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
+                                  void* stream) {
+  // every host-side check of q4llm_step first, and the size limit, before any HIP call
+  size_t need = 0;
+  if (int st = q4llm_step_workspace_bytes(m, C, L, &need)) return st;
+  if (need > Q4LLM_NOALLOC_SCRATCH_BYTES) return Q4_ERR_WORKSPACE;
+  if (!tokens || !start || !last || !caches || !next) return Q4_ERR_NULL;
+  void* ws = nullptr;
+  if (int st = scratch_address(stream, &ws)) return st;
+  // No part of the workspace has to start at zero: every kernel of the step writes each scratch
+  // value it later reads within the same call.
+  return q4llm_step(m, tokens, C, start, last, caches, L, next, logits, ws, Q4LLM_NOALLOC_SCRATCH_BYTES, stream);
 }
