@@ -5,10 +5,14 @@
 
 Headline (the JSON line's `value`): BASELINE config 2, the int4 decode GEMV y = W x at N=5120,
 K=3072 (fused qkv), group 128, fp16 x / fp16 y, fp32 accumulation, in achieved HBM GB/s. A step is
-one GEMV launch over one weight copy; the timed region replays launches over >= 64 rotating weight
-copies (>= 520 MB, twice the 256 MB MALL) so every launch streams its weights from HBM. Launches are
-replayed from a HIP graph so the host does not throttle them; K steps are timed with HIP events on
-the launch stream, bracketed by device synchronisation. Inputs are resident in HBM before timing.
+one GEMV launch over one weight copy. Launches rotate over >= 64 weight copies (>= 520 MB, twice the
+256 MB MALL), so every launch streams its weights from HBM. The timed region is exactly K launches
+(--steps), replayed from a HIP graph so the host does not throttle them and bracketed by HIP events on
+the launch stream after a device synchronisation; it is repeated --reps times (>= 5) and the line
+reports the median (`value`, `ms_per_step`) and the minimum, as the reference's harness does
+(gemm/harness/vk_gemm_bench.c:426-448). When K is smaller than the rotation, the rest of the rotation
+runs untimed between repetitions, so no timed launch finds its copy in the MALL. Inputs are resident
+in HBM before timing.
 
 Other legs (extra JSON fields): the other config-2 GEMV shapes; measured streaming-read and
 empty-kernel probes (the measured roofline and the launch floor); the config-3 fp16 GEMM shapes in
@@ -18,6 +22,10 @@ greedy tokens, buckets 256..4096) in tokens/s with its HBM roofline fraction.
 
 `cpu_baseline` times the reference-faithful CPU path of the headline workload (the oracle's
 QLinear: F.linear over a per-call dequantized fp32 weight, llama_q4.py:72) on this host's cores.
+Every other leg carries its own CPU figure on the same host: the GEMM leg the fp32 host matmul that
+is also its parity reference (gemm/shapes.py:62), the attention leg the oracle's attention block
+(llama_q4.py:224-232), and the 3B leg the oracle's whole step with per-call dequant over a stated
+number of decode steps.
 """
 
 import argparse
@@ -41,6 +49,9 @@ MALL_BYTES = 256 * 2 ** 20
 # FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 20.0 KiB x 1.0.
 # Counters cannot be read inside a timed run, so the figure is carried here with its source.
 GEMV_TRAFFIC_BYTES_5120x3072 = 8_232_858
+# Average kernel duration of the 5120x3072 launch in the rocprofv3 kernel trace of this bench's GEMV
+# leg (profiles/q4_gemv_5120x3072_kernel_stats.md); reported beside the live HIP-event figure.
+GEMV_ROCPROF_AVG_US = 3.486
 
 
 def log(*a):
@@ -52,34 +63,121 @@ def gemv_bytes(N, K, group, x_bytes=2, y_bytes=2):
     return N * K // 2 + N * (K // group) * 2 + K * x_bytes + N * y_bytes
 
 
-def graph_time(fn_list, steps, warmup):
-    """Average ms per launch of launch closures captured into one HIP graph and replayed: the
-    replays are bracketed by HIP events on the capture stream, after a device synchronisation."""
+STREAM_TIMING_MAX_STEPS = 256
+
+
+def timed_steps(fn_list, steps, warmup, reps=7):
+    """Time exactly `steps` launches, `reps` times; launch i is fn_list[i % n] (a rotation over n
+    buffers). Returns the ms per launch of each repetition.
+
+    Before every repetition one untimed pass over the rotation runs, so each buffer's previous use
+    is n - 1 launches back (the MALL holds none of them). The timed region is bracketed by HIP events
+    on the launch stream, and all repetitions are queued before the host waits:
+      * steps <= STREAM_TIMING_MAX_STEPS: the region is `steps` plain stream launches, queued behind a
+        device-side wait (q4_probe_wait) long enough for the host to queue the whole region first;
+        after queueing, the start event must still be pending, which proves no launch of the region
+        waited for the host (else the repetition is re-queued with a longer wait);
+      * larger `steps`: the region is one replay of a HIP graph of the `steps` launches (its ~10 us
+        of graph-launch cost is then under 0.5% of the region)."""
     import torch
+    from q4llm._lib import LIB
+    n = len(fn_list)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for f in fn_list:
             f()
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        for f in fn_list:
-            f()
-    n = len(fn_list)
-    reps = max(1, -(-steps // n))
+
+    def capture(idx):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in idx:
+                fn_list[i % n]()
+        return g
+
+    rot = capture(range(n))
+    stream_mode = steps <= STREAM_TIMING_MAX_STEPS
+    ga = None if stream_mode else capture(range(steps))
+    out = []
     with torch.cuda.stream(s):
         for _ in range(max(1, -(-warmup // n))):
-            g.replay()
+            rot.replay()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(reps):
-            g.replay()
-        e1.record(s)
-        e1.synchronize()
+        if stream_mode:
+            # host cost of queueing one launch, measured with the device busy
+            LIB.call("q4_probe_wait", 20000, s.cuda_stream)
+            t0 = time.perf_counter()
+            for i in range(min(steps, n)):
+                fn_list[i]()
+            host_us = (time.perf_counter() - t0) * 1e6 / min(steps, n)
+            torch.cuda.synchronize()
+            wait_us = int(2 * steps * host_us + 500)
+            events = []
+            while len(out) < reps:
+                LIB.call("q4_probe_wait", min(wait_us, 1000000), s.cuda_stream)
+                rot.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                for i in range(steps):
+                    fn_list[i % n]()
+                e1.record(s)
+                queued_in_time = not e0.query()
+                e1.synchronize()
+                if queued_in_time:
+                    out.append(e0.elapsed_time(e1) / steps)
+                elif wait_us >= 1000000:
+                    raise RuntimeError("timed region could not be queued ahead of the device")
+                else:
+                    wait_us *= 2
+        else:
+            events = []
+            for _ in range(reps):
+                rot.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                ga.replay()
+                e1.record(s)
+                events.append((e0, e1))
+            events[-1][1].synchronize()
+            out = [e0.elapsed_time(e1) / steps for e0, e1 in events]
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * n), reps * n
+    del rot, ga
+    return out
+
+
+def stats_us(ms_list):
+    """median / min / max in microseconds of per-launch times given in ms."""
+    import statistics
+    us = [m * 1e3 for m in ms_list]
+    return {"median": round(statistics.median(us), 3), "min": round(min(us), 3), "max": round(max(us), 3),
+            "reps": len(us)}
+
+
+def under_profiler():
+    """True inside rocprofv3 (its tool library is preloaded into this process and every child)."""
+    return "librocprofiler-sdk" in os.environ.get("LD_PRELOAD", "") or bool(os.environ.get("ROCP_TOOL_LIBRARIES"))
+
+
+def cpu_threads():
+    import torch
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_time_ms(fn, reps=3, budget_s=10.0):
+    """Median wall time of fn() in ms on the host (one untimed call first; fewer reps past the budget)."""
+    import statistics
+    fn()
+    ts, t_all = [], time.perf_counter()
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+        if time.perf_counter() - t_all > budget_s:
+            break
+    return statistics.median(ts), len(ts)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -109,8 +207,8 @@ class GemvBench:
         return [lambda q=q, s=s: ops.q4_gemv_cfg(q, s, self.x, self.group, self.y, cfg=cfg)
                 for q, s in zip(self.qws, self.scs)]
 
-    def time(self, steps, warmup, cfg=-1):
-        return graph_time(self.launches(cfg), steps, warmup)
+    def time(self, steps, warmup, cfg=-1, reps=7):
+        return timed_steps(self.launches(cfg), steps, warmup, reps)
 
     def check(self):
         """max|y - y_ref| / rms(y_ref) against the fp64 CPU oracle (bar: 1e-2)."""
@@ -130,7 +228,7 @@ def probe_read(dev, nbytes, loads):
     sink = torch.empty(1, dtype=torch.float32, device=dev)
     fns = [lambda b=b: LIB.call("q4_probe_read", b.data_ptr(), nbytes, sink.data_ptr(), loads,
                                 torch.cuda.current_stream().cuda_stream) for b in bufs]
-    ms, _ = graph_time(fns, 512, 64)
+    ms = stats_us(timed_steps(fns, 512, 64, 5))["median"] / 1e3
     return ms * 1e3, nbytes / ms / 1e6
 
 
@@ -138,7 +236,7 @@ def probe_empty(grid, block=256):
     import torch
     from q4llm._lib import LIB
     fns = [lambda: LIB.call("q4_probe_empty", grid, block, torch.cuda.current_stream().cuda_stream)] * 64
-    return graph_time(fns, 512, 64)[0] * 1e3
+    return stats_us(timed_steps(fns, 512, 64, 5))["median"]
 
 
 def cpu_gemv_baseline(N, K, group, seconds=10.0):
@@ -147,8 +245,7 @@ def cpu_gemv_baseline(N, K, group, seconds=10.0):
     import torch
     from oracle import llama_q4_ref as R
     from q4llm import synth
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
+    cores = cpu_threads()
     qw, sc, x = synth.gemv_problem(N, K, group)
     ql = R.QLinearRef(group=group, qweight=torch.from_numpy(qw), scales=torch.from_numpy(sc), cache=False)
     xf = torch.from_numpy(x.astype(np.float32)).reshape(1, K)
@@ -180,9 +277,12 @@ GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 
                (4096, 4096, 4096), (1, 3072, 3072)]
 
 
-def bench_gemm(dev, shapes=GEMM_SHAPES):
+def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
+    """Config 3. Parity against the host fp32 matmul of the same fp16 inputs (gemm/shapes.py:62), whose
+    wall time on this host's cores is the leg's CPU figure; error is max|C - ref| / rms(ref)."""
     import torch
     from q4llm import ops, synth
+    cores = cpu_threads()
     out = {}
     for (M, N, K) in shapes:
         a, b = synth.gemm_problem(M, N, K, seed=0)
@@ -191,30 +291,47 @@ def bench_gemm(dev, shapes=GEMM_SHAPES):
         nb = max(4, -(-2 * MALL_BYTES // (2 * N * K))) if M <= 256 else 2
         Bs = [B0.clone() for _ in range(nb)]
         C = torch.empty(M, N, dtype=torch.float16, device=dev)
-        ref = A.float() @ B0.float().T
+        C.fill_(float("nan"))
         ops.gemm_f16_nt(A, B0, out=C)
-        err = (C.float() - ref).abs().max().item() / ref.pow(2).mean().sqrt().item()
-        del ref
+        got = C.cpu().float()
+        a32, b32 = torch.from_numpy(a).float(), torch.from_numpy(b).float()
+        ref_box = {}
+
+        def host_ref():
+            ref_box["r"] = a32 @ b32.T
+
+        cpu_ms, cpu_n = cpu_time_ms(host_ref, reps=3, budget_s=8.0)
+        ref = ref_box["r"]
+        err = (got - ref).abs().max().item() / ref.pow(2).mean().sqrt().item()
+        del ref, ref_box, got
         fns = [lambda B=B: ops.gemm_f16_nt(A, B, out=C) for B in Bs]
-        ms, _ = graph_time(fns, max(16, len(fns) * 4), len(fns))
+        st = stats_us(timed_steps(fns, max(16, len(fns) * 2), len(fns), reps))
+        ms = st["median"] / 1e3
         flops = 2.0 * M * N * K
         byts = 2.0 * (M * K + N * K + M * N)
         tf = flops / ms / 1e9
         attain = min(MFMA_F16_PEAK_TFLOPS, flops / byts * HBM_PEAK_GBS / 1e3)
-        out[f"{M}x{N}x{K}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+        out[f"{M}x{N}x{K}"] = {"us": st["median"], "us_min": st["min"], "reps": st["reps"], "TFLOP/s": round(tf, 1),
                                "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                                "attainable_TFLOP/s": round(attain, 1), "frac_attainable": round(tf / attain, 4),
-                               "GB/s": round(byts / ms / 1e6, 1), "err_over_rms": float(f"{err:.3e}")}
-        log(f"gemm {M}x{N}x{K}: {ms * 1e3:.2f} us {tf:.1f} TFLOP/s ({tf / attain:.1%} of attainable {attain:.0f})")
+                               "GB/s": round(byts / ms / 1e6, 1), "err_over_rms": float(f"{err:.3e}"),
+                               "cpu_ms": round(cpu_ms, 3), "cpu_TFLOP/s": round(flops / cpu_ms / 1e9, 3),
+                               "cpu_cores": cores, "cpu_reps": cpu_n}
+        log(f"gemm {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}) {tf:.1f} TFLOP/s "
+            f"({tf / attain:.1%} of attainable {attain:.0f}); host fp32 {cpu_ms:.2f} ms; err/rms {err:.2e}")
         del A, B0, Bs, C
         torch.cuda.empty_cache()
     return out
 
 
-def bench_attn(dev):
+def bench_attn(dev, reps=5):
+    """Config 4 (24/8 heads, hd 128, one query row at position valid - 1). CPU figure: the oracle's
+    attention block (llama_q4.py:224-232) over the same caches on this host's cores."""
     import math
     import torch
+    from oracle import llama_q4_ref as R
     from q4llm import ops, synth
+    cores = cpu_threads()
     out = {}
     for L in (256, 512, 1024, 2048, 4096):
         q, k, v, valid = synth.attn_problem(L, seed=0)
@@ -228,13 +345,19 @@ def bench_attn(dev):
         o = torch.empty(1, 24 * 128, dtype=torch.float32, device=dev)
         fns = [lambda kk=kk, vv=vv: ops.attn_bucket(qd, kk, vv, L, start, 1 / math.sqrt(128), ws, o)
                for kk, vv in zip(ks, vs)]
-        ms, _ = graph_time(fns, max(64, len(fns)), len(fns))
+        st = stats_us(timed_steps(fns, max(64, len(fns)), len(fns), reps))
+        ms = st["median"] / 1e3
+        qc, kc, vc = torch.from_numpy(q).reshape(1, 24, 128), torch.from_numpy(k), torch.from_numpy(v)
+        allowed = torch.arange(L)[None, :] <= valid - 1
+        cpu_ms, _ = cpu_time_ms(lambda: R.attention(qc, kc, vc, allowed, L, 1 / math.sqrt(128)), reps=5, budget_s=3.0)
         byts = 2 * valid * 8 * 128 * 2 + 24 * 128 * 4 * 2
         gbs = byts / ms / 1e6
-        out[f"L{L}"] = {"valid": valid, "us": round(ms * 1e3, 2), "GB/s_valid_rows": round(gbs, 1),
-                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                        "GB/s_bucket": round((2 * L * 8 * 128 * 2) / ms / 1e6, 1)}
-        log(f"attn L={L} valid={valid}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s over valid rows")
+        out[f"L{L}"] = {"valid": valid, "us": st["median"], "us_min": st["min"], "reps": st["reps"],
+                        "GB/s_valid_rows": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                        "GB/s_bucket": round((2 * L * 8 * 128 * 2) / ms / 1e6, 1),
+                        "cpu_us": round(cpu_ms * 1e3, 1), "cpu_cores": cores}
+        log(f"attn L={L} valid={valid}: {st['median']:.2f} us (min {st['min']:.2f}), {gbs:.0f} GB/s over valid rows; "
+            f"CPU oracle {cpu_ms * 1e3:.0f} us")
         del ks, vs
         torch.cuda.empty_cache()
     return out
@@ -248,7 +371,36 @@ LAYER_BYTES_3B = 51_904_512     # wqkv + wo + wgu + wdown packed weights + fp16 
 LM_HEAD_BYTES_3B = 203_157_504  # tied int4 embedding as the LM head
 
 
-def bench_e2e(dev, n_new=256, native=True):
+def cpu_decode_baseline(pc, host_tensors, token, pos=700, L=1024, max_steps=3, budget_s=20.0):
+    """The reference's eager decode step on this host's cores: the oracle's LlamaQ4.step with every
+    QLinear re-dequantizing its weight per call (llama_q4.py:72,199-239), over the same quantized
+    weights as the GPU run, at the bucket and position the GPU decode uses. One step takes tens of
+    seconds (each step dequantizes 1.66 GB of int4 weights), so at least one and at most `max_steps`
+    steps are timed, stopping once `budget_s` has passed."""
+    import torch
+    from oracle import llama_q4_ref as R
+    cores = cpu_threads()
+    ref = R.LlamaQ4Ref.from_quantized(pc, host_tensors, cache=False)
+    caches = ref.new_caches()
+    tok = torch.tensor([[token]], dtype=torch.int32)
+    ts = []
+    for i in range(max_steps):
+        if sum(ts) > budget_s:
+            break
+        t0 = time.perf_counter()
+        nxt, _ = ref.step(tok, torch.tensor([pos + i], dtype=torch.int32), torch.tensor([0], dtype=torch.int32),
+                          caches, L)
+        ts.append(time.perf_counter() - t0)
+        tok = nxt.reshape(1, 1)
+    steps = len(ts)
+    return {"decode_tok_s": round(steps / sum(ts), 4), "s_per_step": round(sum(ts) / steps, 3), "steps_timed": steps,
+            "cores": cores, "kind": "port", "L": L,
+            "sample": f"{steps} decode steps of the oracle LlamaQ4.step at L={L} from position {pos}, per-call "
+                      "dequant of every int4 weight (eager QLinear.forward), same quantized weights"}
+
+
+def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
+    import statistics
     import torch
     from q4llm import llm_runner, synth
     from q4llm.llama_q4 import LlamaQ4
@@ -263,22 +415,24 @@ def bench_e2e(dev, n_new=256, native=True):
     buckets = [256, 512, 1024, 2048, 4096]
     caches = model.new_caches()
     res = llm_runner.run(model, prompt, n_new, 256, buckets, caches=caches)
-    # GPU-only time of one decode step at the bucket the run used (graph replays back to back)
+    # GPU-only time of one decode step at the bucket the run used: graph replays back to back, the
+    # median and minimum over `reps` repetitions of 50 replays
     g = model.entry_point(1, 1024, caches)
-    g.start.fill_(700)
-    g.tokens.fill_(res["tokens"][-1])
-    torch.cuda.synchronize()
     s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    g.replay()
-    torch.cuda.synchronize()
-    e0.record(s)
-    reps = 50
+    per = []
     for _ in range(reps):
+        g.start.fill_(700)
+        g.tokens.fill_(res["tokens"][-1])
         g.replay()
-    e1.record(s)
-    e1.synchronize()
-    gpu_ms = e0.elapsed_time(e1) / reps
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(50):
+            g.replay()
+        e1.record(s)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) / 50)
+    gpu_ms = statistics.median(per)
     n_layers = synth.LLAMA32_3B["num_hidden_layers"]
     w_bytes = n_layers * LAYER_BYTES_3B + LM_HEAD_BYTES_3B
     avg_valid = 512 + (n_new - 1) / 2 + 1
@@ -288,7 +442,7 @@ def bench_e2e(dev, n_new=256, native=True):
     out = {
         "decode_tok_s": tok_s, "prefill_tok_s": res["prefill_tok_s"], "ttft_ms": res["ttft_ms"],
         "decode_steps": res["decode_steps"], "gpu_ms_per_decode_step": round(gpu_ms, 4),
-        "gpu_only_tok_s": round(1e3 / gpu_ms, 1),
+        "gpu_ms_per_decode_step_min": round(min(per), 4), "gpu_only_tok_s": round(1e3 / gpu_ms, 1),
         "bytes_per_step_valid_kv": int(w_bytes + kv_valid), "bytes_per_step_bucket_L1024": int(w_bytes + kv_bucket),
         "hbm_roofline_tok_s_L1024": round(HBM_PEAK_GBS * 1e9 / (w_bytes + kv_bucket), 1),
         "frac_hbm_roofline": round(tok_s * (w_bytes + kv_valid) / (HBM_PEAK_GBS * 1e9), 4),
@@ -298,37 +452,54 @@ def bench_e2e(dev, n_new=256, native=True):
         "buckets_used": sorted({L for L, _ in res["steps"]}),
     }
     log(f"e2e decode {tok_s:.1f} tok/s (GPU-only {1e3 / gpu_ms:.1f}), prefill {res['prefill_tok_s']:.0f} tok/s")
-    if not native:
-        del model, caches
+    host = None
+    if cpu:
+        host = {k: v.cpu() for k, v in model.packed_tensors().items()}
+        pc = model.packed_config()
+    if native and under_profiler():
+        # the runner's HIP runtime crashes in the profiler's preloaded tool (observed under rocprofv3)
+        log("e2e native runner: skipped under rocprofv3")
+        out["native_runner"] = "skipped under a profiler"
+        native = False
+    if native:
+        # the same generation through the native runner (lib/llm-runner) from the packed weights
+        import tempfile
+        from q4llm import sweep
+        with tempfile.TemporaryDirectory() as td:
+            wpath = pathlib.Path(td) / "llama32_3b_shape.q4w"
+            model.save_packed(wpath)
+            del model, caches, g
+            torch.cuda.empty_cache()
+            nat = sweep.run_runner(wpath, prompt, n_new, 256, ",".join(map(str, buckets)), "bucketed")
+        out.update(native_runner_decode_tok_s=nat["decode_tok_s"], native_runner_prefill_tok_s=nat["prefill_tok_s"],
+                   native_runner_ttft_ms=nat["ttft_ms"], native_runner_tokens_match=nat["tokens"] == res["tokens"])
+        log(f"e2e native runner: decode {nat['decode_tok_s']:.1f} tok/s, prefill {nat['prefill_tok_s']:.0f} tok/s, "
+            f"tokens match: {nat['tokens'] == res['tokens']}")
+    else:
+        del model, caches, g
         torch.cuda.empty_cache()
-        return out, res["tokens"]
-    # the same generation through the native runner (lib/llm-runner) from the packed weights
-    import tempfile
-    from q4llm import sweep
-    with tempfile.TemporaryDirectory() as td:
-        wpath = pathlib.Path(td) / "llama32_3b_shape.q4w"
-        model.save_packed(wpath)
-        del model, caches
-        torch.cuda.empty_cache()
-        nat = sweep.run_runner(wpath, prompt, n_new, 256, ",".join(map(str, buckets)), "bucketed")
-    out.update(native_runner_decode_tok_s=nat["decode_tok_s"], native_runner_prefill_tok_s=nat["prefill_tok_s"],
-               native_runner_ttft_ms=nat["ttft_ms"], native_runner_tokens_match=nat["tokens"] == res["tokens"])
-    log(f"e2e native runner: decode {nat['decode_tok_s']:.1f} tok/s, prefill {nat['prefill_tok_s']:.0f} tok/s, "
-        f"tokens match: {nat['tokens'] == res['tokens']}")
+    if host is not None:
+        log("e2e CPU baseline (oracle step, per-call dequant) ...")
+        cb = cpu_decode_baseline(pc, host, res["tokens"][-1])
+        del host
+        cb["gpu_over_cpu"] = round(tok_s / cb["decode_tok_s"], 1)
+        out["cpu_baseline"] = cb
+        log(f"e2e CPU baseline: {cb['decode_tok_s']} tok/s on {cb['cores']} cores ({cb['s_per_step']} s per step)")
     return out, res["tokens"]
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=2048, help="timed launches per repetition of the headline GEMV")
+    ap.add_argument("--warmup", type=int, default=256, help="untimed launches before timing")
+    ap.add_argument("--reps", type=int, default=7, help="timed repetitions (median and min are reported; >= 5)")
     ap.add_argument("--skip-e2e", action="store_true")
-    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true", help="leave out every CPU-baseline figure")
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attn", action="store_true")
     ap.add_argument("--skip-native", action="store_true",
-                    help="skip the native-runner e2e leg (a child process: leave it out under a profiler)")
+                    help="skip the native-runner e2e leg (also skipped by itself under rocprofv3)")
     ap.add_argument("--sweep-gemv", action="store_true", help="time every GEMV tile config (tuning)")
     ap.add_argument("--gemm-shapes", nargs="*", default=None, metavar="MxNxK",
                     help="run the GEMM leg on these shapes only (default: every config-3 shape)")
@@ -337,6 +508,9 @@ def main():
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported: this build runs on a single "
               "MI355X and multi-GPU sharding is design-only", file=sys.stderr)
+        return 2
+    if a.steps < 1 or a.reps < 5:
+        print("--steps must be >= 1 and --reps >= 5", file=sys.stderr)
         return 2
 
     import torch
@@ -354,12 +528,15 @@ def main():
         rel = gb.check()
         if a.sweep_gemv:
             for cfg in range(LIB.raw("q4_gemv_num_configs")()):
-                ms, _ = gb.time(512, 64, cfg=cfg)
+                ms = stats_us(gb.time(512, 64, cfg=cfg, reps=5))["median"] / 1e3
                 log(f"sweep N={N} K={K} cfg={cfg}: {ms * 1e3:.2f} us {gb.bytes / ms / 1e6:.0f} GB/s")
         steps = a.steps if (N, K) == shapes[0] else max(256, a.steps // 4)
-        ms, n = gb.time(steps, a.warmup)
-        results[(N, K)] = dict(us=ms * 1e3, gbs=gb.bytes / ms / 1e6, bytes=gb.bytes, err=rel, launches=n)
-        log(f"gemv N={N} K={K}: {ms * 1e3:.3f} us/launch, {gb.bytes / ms / 1e6:.1f} GB/s, err/rms {rel:.2e}")
+        st = stats_us(gb.time(steps, a.warmup, reps=a.reps))
+        us = st["median"]
+        results[(N, K)] = dict(us=us, us_min=st["min"], us_max=st["max"], reps=st["reps"], gbs=gb.bytes / us / 1e3,
+                               bytes=gb.bytes, err=rel, steps=steps, copies=len(gb.qws))
+        log(f"gemv N={N} K={K}: {us:.3f} us/launch (min {st['min']:.3f}, max {st['max']:.3f} over {st['reps']} reps "
+            f"of {steps}), {gb.bytes / us / 1e3:.1f} GB/s, err/rms {rel:.2e}")
         del gb
         torch.cuda.empty_cache()
 
@@ -379,7 +556,7 @@ def main():
         "value": round(head["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": head["launches"],
+        "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(head["us"] / 1e3, 6),
         "higher_is_better": True,
@@ -388,15 +565,22 @@ def main():
         "dtype": "int4 weights, fp16 x/y, fp32 accumulate",
         "data": "synthetic (seeded numpy: nibbles U[0,15], group-128 scales |N(0,0.01)| fp16, x N(0,1) fp16)",
         "config": {"workload": "int4 decode GEMV y=Wx, N=5120 (fused qkv), K=3072, group 128, batch 1",
-                   "N": 5120, "K": 3072, "group": 128, "weight_copies_rotated": 64},
+                   "N": 5120, "K": 3072, "group": 128, "weight_copies_rotated": head["copies"]},
+        "timing": {"statistic": "median over repetitions of the timed region (value, ms_per_step)",
+                   "reps": head["reps"], "steps_per_rep": head["steps"], "us_per_step_median": head["us"],
+                   "us_per_step_min": head["us_min"], "us_per_step_max": head["us_max"]},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES_5120x3072,
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
+                     "frac_at_min": round(head["bytes"] / head["us_min"] / 1e3 / HBM_PEAK_GBS, 4),
+                     "traffic": GEMV_TRAFFIC_BYTES_5120x3072,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
                      "algorithmic_bytes_per_launch": head["bytes"], "avg_launch_us": round(head["us"], 4),
+                     "rocprof_avg_kernel_us": GEMV_ROCPROF_AVG_US,
+                     "frac_at_rocprof_avg": round(head["bytes"] / GEMV_ROCPROF_AVG_US / 1e3 / HBM_PEAK_GBS, 4),
                      "measured_read_floor_us_same_bytes": floor,
                      "frac_of_measured_read_floor": round(floor / head["us"], 4)},
-        "gemv_shapes": {f"{N}x{K}": {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
-                                      "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+        "gemv_shapes": {f"{N}x{K}": {"us": round(r["us"], 3), "us_min": round(r["us_min"], 3),
+                                      "GB/s": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
                                       "err_over_rms": float(f"{r['err']:.3e}")} for (N, K), r in results.items()},
         "measured_probes": probes,
     }
@@ -407,7 +591,7 @@ def main():
     if not a.skip_attn:
         out["attn_decode"] = bench_attn(dev)
     if not a.skip_e2e:
-        e2e, tokens = bench_e2e(dev, native=not a.skip_native)
+        e2e, tokens = bench_e2e(dev, native=not a.skip_native, cpu=not a.skip_cpu)
         out["e2e_3b"] = e2e
         if a.tokens_out:
             pathlib.Path(a.tokens_out).write_text(json.dumps(tokens))

@@ -271,6 +271,11 @@ int q4llm_advance_position(int32_t* start, int delta, void* stream);
 int q4_probe_read(const void* buf, int64_t bytes, float* sink, int loads_per_thread, void* stream);
 /* Empty kernel launch (launch-floor probe). */
 int q4_probe_empty(int grid, int block, void* stream);
+/* One wave that sleeps on the device for about `microseconds` (0 .. 1 s; bounded by the constant-rate
+ * real-time counter and by a sleep count): lets a benchmark queue a timed region on `stream` before
+ * the device reaches it, so host latency stays out of the region (the harness's warm-up spacing,
+ * gemm/harness/vk_gemm_bench.c:426-448). */
+int q4_probe_wait(int64_t microseconds, void* stream);
 /* Number of entries in the explicit GEMV / GEMM tile lists, and the same entry points with a
  * forced entry (cfg < 0: automatic) and, for the GEMV, a grid (0: automatic; grid-stride entries
  * only). gemm_f16_nt_cfg's `split` is reserved and must be 0. */

@@ -29,6 +29,17 @@ __global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ buf
 
 __global__ void empty_kernel() {}
 
+// One wave that sleeps until `ticks` of the constant-rate real-time counter (s_memrealtime) have
+// passed since it started, or until `max_iter` sleeps, whichever comes first: a bounded stretch of
+// device time that lets the host queue a timed region before the device reaches it.
+__global__ void wait_kernel(uint64_t ticks, uint64_t max_iter) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (uint64_t i = 0; i < max_iter; ++i) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+    __builtin_amdgcn_s_sleep(32);
+  }
+}
+
 }  // namespace
 }  // namespace q4
 
@@ -55,5 +66,20 @@ extern "C" int q4_probe_read(const void* buf, int64_t bytes, float* sink, int lo
 extern "C" int q4_probe_empty(int grid, int block, void* stream) {
   if (grid <= 0 || block <= 0 || block > 1024) return Q4_ERR_SHAPE;
   hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, as_stream(stream));
+  return launch_status();
+}
+
+extern "C" int q4_probe_wait(int64_t microseconds, void* stream) {
+  if (microseconds < 0 || microseconds > 1000 * 1000) return Q4_ERR_RANGE;
+  int dev = 0, khz = 0;
+  Q4_CHECK_HIP(hipGetDevice(&dev));
+  Q4_CHECK_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  if (khz <= 0) return Q4_ERR_UNSUPPORTED;
+  const uint64_t ticks = static_cast<uint64_t>(microseconds) * static_cast<uint64_t>(khz) / 1000;
+  // s_sleep 32 lasts about 32 * 64 shader clocks (0.85 us at 2.4 GHz), so the sleep cap lets the
+  // counter end the loop at any clock down to ~1.4 GHz and ends it by itself within ~7x the request
+  // even at a quarter of 2.4 GHz
+  const uint64_t max_iter = static_cast<uint64_t>(microseconds) * 2 + 64;
+  hipLaunchKernelGGL(wait_kernel, dim3(1), dim3(64), 0, as_stream(stream), ticks, max_iter);
   return launch_status();
 }

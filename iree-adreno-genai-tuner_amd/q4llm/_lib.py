@@ -56,6 +56,7 @@ SIGNATURES = {
     "q4llm_step_noalloc": [p, p, i32, p, p, p, i32, p, p, p],
     "q4_probe_read": [p, i64, p, i32, p],
     "q4_probe_empty": [i32, i32, p],
+    "q4_probe_wait": [i64, p],
 }
 _RESTYPES = {"q4llm_status_string": C.c_char_p}
 

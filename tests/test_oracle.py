@@ -251,3 +251,29 @@ def test_oracle_rope_tables_match_closed_form_default():
     ang = np.concatenate([ang, ang], 1)
     assert np.allclose(cos.numpy(), np.cos(ang), atol=2e-6)
     assert np.allclose(sin.numpy(), np.sin(ang), atol=2e-6)
+
+
+def test_from_quantized_per_call_dequant_equals_cached_model():
+    """LlamaQ4Ref.from_quantized over a model's own quantized tensors, re-dequantizing every weight per
+    call (the reference's eager QLinear.forward, llama_q4.py:72), gives the same logits bit for bit as
+    the model built from the dense state dict with cached dequantized weights."""
+    from q4llm import synth
+    cfg = synth.TINY
+    sd = synth.SyntheticWeights(cfg, 1, std=0.2)
+    dense = {k: sd[k] for k in sd.keys()}
+    ref = R.LlamaQ4Ref(cfg, dense, group=32, max_ctx=64)
+    t = {"embed.qweight": ref.embed.qweight, "embed.scales": ref.embed.scales, "ln_f": ref.ln_f,
+         "cos": ref.cos, "sin": ref.sin}
+    for i, ly in enumerate(ref.layers):
+        for nm in ("wqkv", "wo", "wgu", "wdown"):
+            t[f"layers.{i}.{nm}.qweight"], t[f"layers.{i}.{nm}.scales"] = ly[nm].qweight, ly[nm].scales
+        t[f"layers.{i}.ln_in"], t[f"layers.{i}.ln_post"] = ly["ln_in"], ly["ln_post"]
+    pc = dict(dim=ref.dim, n_layers=ref.n_layers, n_heads=ref.n_heads, n_kv=ref.n_kv, head_dim=ref.head_dim,
+              inter=ref.inter, vocab=ref.embed.vocab, group=32, max_ctx=64, eps=ref.eps)
+    eager = R.LlamaQ4Ref.from_quantized(pc, t, cache=False)
+    assert all(ly["wqkv"]._w is None for ly in eager.layers)
+    toks = torch.tensor([synth.prompt_ids(8, 1024, seed=2)], dtype=torch.int32)
+    args = (torch.tensor([0], dtype=torch.int32), torch.tensor([7], dtype=torch.int32))
+    n1, l1 = ref.step(toks, *args, ref.new_caches(), 16)
+    n2, l2 = eager.step(toks, *args, eager.new_caches(), 16)
+    assert torch.equal(l1, l2) and torch.equal(n1, n2)
