@@ -125,6 +125,36 @@ int q4_gemv_epilogue(const int32_t* qweight, const uint16_t* scales, const float
                      const float* aux, float eps, int epilogue, const q4_rope_kv* rope, float* y, int64_t N,
                      int64_t K, int group, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * T16: the decode GEMV's device copy of an int4 weight (no counterpart in the reference, whose
+ * [N, K/8] layout stays the interface; built once from it at load time)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Row pairing of a T16 copy: which rows share a 16-row tile, matching the GEMV epilogue it feeds. */
+enum { Q4_PAIR_NONE = 0, Q4_PAIR_SWIGLU = 1, Q4_PAIR_ROPE = 2 };
+
+/* Bytes of the T16 copy of an [N, K] weight with `group` (32 or 128) and `pairing` (Q4_PAIR_ROPE
+ * takes head_dim; the others ignore it): tiles [ceil(rows/16)][K padded to 4 groups / 128][16][64 B]
+ * and scales [ceil(rows/16)][tiles of 4 groups][4][16] fp16. Q4_ERR_UNSUPPORTED when the decode
+ * GEMV does not take the shape (the caller keeps the reference layout for it). */
+int q4_t16_bytes(int64_t N, int64_t K, int group, int pairing, int head_dim, size_t* tile_bytes,
+                 size_t* scale_bytes);
+
+/* Writes the T16 copy of (qweight [N, K/8] int32, scales [N, K/group] fp16): each 16-row tile holds
+ * its rows' 128-k segments as contiguous 1 KB blocks, in the row order of the GEMV's 16-row blocks
+ * (Q4_PAIR_SWIGLU: pairs p with rows p and p + N/2; Q4_PAIR_ROPE: rows (head, d) and
+ * (head, d + head_dim/2) of the fused qkv weight); padding is zero. A permutation of the bytes. */
+int q4_t16_pack(const int32_t* qweight, const uint16_t* scales, int64_t N, int64_t K, int group,
+                int pairing, int head_dim, void* tiles, void* tile_scales, void* stream);
+
+/* Decode GEMV on a T16 copy, fp32 x and y: the same results as q4_gemv / q4_gemv_fused /
+ * q4_gemv_epilogue on the reference layout (QLinear._gemv_fused, llama_q4.py:74-90) with prologue
+ * Q4_PRO_NONE or Q4_PRO_RMSNORM and epilogue 0 (plain, optional fp32 residual), Q4_EPI_SWIGLU or
+ * Q4_EPI_ROPE_KV (rope required), the copy packed with the matching pairing. x must not alias y. */
+int q4_gemv_t16(const void* tiles, const void* tile_scales, const float* x, int prologue,
+                const float* aux, float eps, int epilogue, const q4_rope_kv* rope, float* y,
+                const float* residual, int64_t N, int64_t K, int group, void* stream);
+
 /* Prefill projection, replaces QLinear.forward at M > 1 (llama_q4.py:72,
  * F.linear(x, dequantize_q4(W))): y[M, N] = residual + x[M, K] @ dequant(W)^T, x and y fp32.
  * Runs on the fp16 matrix cores with x split into two fp16 terms and the int4 values exact in
@@ -207,12 +237,21 @@ int argmax_f32(const float* logits, int64_t V, int32_t* out, void* workspace, si
  * decode_logits_l{L}, scripts/llm/export_llama.py:1-10,35-49; LlamaQ4.step llama_q4.py:199-239)
  * ------------------------------------------------------------------------------------------- */
 
+/* Optional T16 copies (q4_t16_pack) of a weight for the decode GEMVs: tiles and tile scales, both
+ * NULL when absent (decode then reads the reference layout). wqkv takes Q4_PAIR_ROPE pairing,
+ * wgu Q4_PAIR_SWIGLU, wo, wdown and the LM head Q4_PAIR_NONE. */
+typedef struct q4llm_t16 {
+  const void* tiles;
+  const void* scales;
+} q4llm_t16;
+
 typedef struct q4llm_layer {
   const int32_t* wqkv_q;  const uint16_t* wqkv_s;   /* [(n_q + 2 n_kv) hd, dim] */
   const int32_t* wo_q;    const uint16_t* wo_s;     /* [dim, n_q hd] */
   const int32_t* wgu_q;   const uint16_t* wgu_s;    /* [2 inter, dim] (gate rows then up rows) */
   const int32_t* wdown_q; const uint16_t* wdown_s;  /* [dim, inter] */
   const float* ln_in;     const float* ln_post;     /* [dim] */
+  q4llm_t16 wqkv_t, wo_t, wgu_t, wdown_t;           /* optional decode copies */
 } q4llm_layer;
 
 typedef struct q4llm_model {
@@ -222,6 +261,7 @@ typedef struct q4llm_model {
   const float* ln_f;                                 /* [dim] */
   const float* cos_t; const float* sin_t;            /* RoPE tables [max_ctx, head_dim] */
   const q4llm_layer* layers;                         /* host array of n_layers */
+  q4llm_t16 embed_t;                                 /* optional decode copy of the LM head */
 } q4llm_model;
 
 /* Workspace bytes for one step with C tokens and bucket L. */
@@ -288,6 +328,18 @@ int gemm_f16_num_configs(void);
 int q4_linear_ws_num_configs(void);
 int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
                     int64_t lda, int64_t ldb, int64_t ldc, int cfg, int split, void* stream);
+/* The entries of the explicit tile lists, for host-side checks of their index mapping (each call
+ * fills `info` and returns Q4_ERR_RANGE past the last entry):
+ *   q4_gemv_config_info:    lanes per row, chunks per lane, rows per lane, waves, x words, grid-stride
+ *   q4_gemv_mx_config_info: row blocks per workgroup, waves per row block, tiles per wave, used rows
+ *                           per 16-row block, grid-stride (q4_gemv_mx_num_configs entries)
+ *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, ping-pong
+ *   q4_linear_ws_config_info: BM, BN, wave rows, wave columns, stages, k-split */
+int q4_gemv_config_info(int cfg, int* info);
+int q4_gemv_mx_num_configs(void);
+int q4_gemv_mx_config_info(int cfg, int* info);
+int gemm_f16_config_info(int cfg, int* info);
+int q4_linear_ws_config_info(int cfg, int* info);
 
 #ifdef __cplusplus
 }

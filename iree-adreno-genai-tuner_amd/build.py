@@ -30,7 +30,7 @@ COMMON = [
 
 LIB_SOURCES = [
     "q4_status.cpp", "q4_format.hip", "q4_gemv.hip", "q4_gemv_mx.hip", "gemm_f16.hip", "q4_linear.hip",
-    "attn_bucket.hip", "llama_ops.hip", "q4llm_step.cpp", "roofline_probe.hip",
+    "attn_bucket.hip", "llama_ops.hip", "q4llm_step.cpp", "roofline_probe.hip", "q4_t16.hip",
 ]
 
 

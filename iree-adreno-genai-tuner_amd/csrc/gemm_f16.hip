@@ -541,6 +541,14 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
 
 int gemm_f16_num_tiles() { return kNumTiles; }
 
+int gemm_f16_tile_info(int i, int* out) {
+  if (i < 0 || i >= kNumTiles) return Q4_ERR_RANGE;
+  const TileCfg& t = kTiles[i];
+  const int v[7] = {t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.pp ? 1 : 0};
+  for (int j = 0; j < 7; ++j) out[j] = v[j];
+  return Q4_OK;
+}
+
 }  // namespace q4
 
 namespace {
@@ -570,3 +578,8 @@ extern "C" int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C
 }
 
 extern "C" int gemm_f16_num_configs(void) { return q4::gemm_f16_num_tiles(); }
+
+extern "C" int gemm_f16_config_info(int cfg, int* info) {
+  if (!info) return Q4_ERR_NULL;
+  return q4::gemm_f16_tile_info(cfg, info);
+}

@@ -432,6 +432,33 @@ int main(int argc, char** argv) {
   m.sin_t = static_cast<const float*>(need(pk, "sin"));
   m.layers = r.layers.data();
 
+  // T16 copies of the decode projections and the LM head (q4_t16_pack), built on the device from the
+  // reference layout; shapes the decode GEMV does not take keep none.
+  auto t16 = [&](const int32_t* q, const uint16_t* sc, int64_t n, int64_t k, int pairing) {
+    q4llm_t16 t{nullptr, nullptr};
+    size_t tb = 0, sb = 0;
+    const int st = q4_t16_bytes(n, k, m.group, pairing, m.head_dim, &tb, &sb);
+    if (st == Q4_ERR_UNSUPPORTED) return t;
+    Q4_OK_OR_DIE(st);
+    void *tiles = nullptr, *tsc = nullptr;
+    HIP_OK(hipMalloc(&tiles, tb));
+    HIP_OK(hipMalloc(&tsc, sb));
+    pk.device_buffers.push_back(tiles);
+    pk.device_buffers.push_back(tsc);
+    Q4_OK_OR_DIE(q4_t16_pack(q, sc, n, k, m.group, pairing, m.head_dim, tiles, tsc, nullptr));
+    t.tiles = tiles;
+    t.scales = tsc;
+    return t;
+  };
+  const int64_t qkv_n = static_cast<int64_t>(m.n_heads + 2 * m.n_kv) * m.head_dim;
+  for (auto& ly : r.layers) {
+    ly.wqkv_t = t16(ly.wqkv_q, ly.wqkv_s, qkv_n, m.dim, Q4_PAIR_ROPE);
+    ly.wgu_t = t16(ly.wgu_q, ly.wgu_s, 2LL * m.inter, m.dim, Q4_PAIR_SWIGLU);
+    ly.wdown_t = t16(ly.wdown_q, ly.wdown_s, m.dim, m.inter, Q4_PAIR_NONE);
+  }
+  m.embed_t = t16(m.embed_q, m.embed_s, m.vocab, m.dim, Q4_PAIR_NONE);
+  HIP_OK(hipDeviceSynchronize());
+
   // KV caches: zeroed device buffers kept for the whole run (llm_runner.c:301-315).
   const size_t cache_bytes = static_cast<size_t>(m.max_ctx) * m.n_kv * m.head_dim * 2;
   r.caches.resize(2 * nl);

@@ -707,7 +707,7 @@ int set_lds_limit(KernelFn fn, size_t bytes) {
 // take. `ep` points at an EpiArgs (same field order as the kernel's own struct).
 int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
                    const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
-                   const void* ep, hipStream_t stream);
+                   const void* ep, hipStream_t stream, bool tiled);
 
 // Runs config `cfg` (-1 = automatic choice) with `grid_override` workgroups (0 = automatic).
 // Automatic fp32-x / fp32-y launches go to the matrix-core kernel when it takes the shape.
@@ -718,7 +718,7 @@ int q4_gemv_launch(const int32_t* qweight, const uint16_t* scales, const void* x
   const bool f16x = x_dtype == Q4_F16, f16y = y_dtype == Q4_F16;
   if (cfg < 0 && !f16x && !f16y && prologue != kProSwiglu) {
     const int st = gemv_mx_launch(qweight, scales, static_cast<const float*>(x), aux, eps, static_cast<float*>(y),
-                                  residual, N, K, group, prologue, epilogue, &ea, stream);
+                                  residual, N, K, group, prologue, epilogue, &ea, stream, false);
     if (st != Q4_ERR_UNSUPPORTED) return st;
   }
   const bool paired = epilogue != kEpiNone;
@@ -800,6 +800,21 @@ extern "C" int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const
 }
 
 extern "C" int q4_gemv_num_configs(void) { return q4::q4_gemv_num_cfgs(); }
+
+namespace q4 {
+int q4_gemv_cfg_info(int i, int* out) {
+  if (i < 0 || i >= kNumCfgs) return Q4_ERR_RANGE;
+  const Cfg& c = kCfgs[i];
+  const int v[6] = {c.lpr, c.cpl, c.r, c.waves, c.xw, c.multi ? 1 : 0};
+  for (int j = 0; j < 6; ++j) out[j] = v[j];
+  return Q4_OK;
+}
+}  // namespace q4
+
+extern "C" int q4_gemv_config_info(int cfg, int* info) {
+  if (!info) return Q4_ERR_NULL;
+  return q4::q4_gemv_cfg_info(cfg, info);
+}
 
 extern "C" int q4_gemv_fused(const int32_t* qweight, const uint16_t* scales, const float* x, int prologue,
                              const float* aux, float eps, float* y, const float* residual, int64_t N, int64_t K,

@@ -64,6 +64,12 @@ __device__ __forceinline__ uint16_t load2(__amdgpu_buffer_rsrc_t r, uint32_t off
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
 
+__device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+  const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y));
+}
+
 constexpr int kProNone = 0, kProNorm = 1;
 constexpr int kEpiNone = 0, kEpiSwiglu = 1, kEpiRope = 2;
 
@@ -217,7 +223,7 @@ __device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, u
 // W = RBW * WPB waves and converts x once for all of them. MULTI: grid-stride over groups of RBW
 // row blocks with the next group's loads in flight. RPB: used rows per 16-row block (16, or 8 to
 // spread a short matrix over more workgroups).
-template <int G, int RBW, int WPB, int TPW, bool MULTI, int PRO, int EPI, int RPB>
+template <int G, int RBW, int WPB, int TPW, bool MULTI, int PRO, int EPI, int RPB, bool TL = false>
 __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const float* __restrict__ x,
     const float* __restrict__ aux, float eps, float* y, const float* residual, int N, int K, int n_tiles,
@@ -243,8 +249,15 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
   const int q = c >> 2, j = c & 3;
   const int kg = K / G;  // real groups
 
-  const __amdgpu_buffer_rsrc_t wres = rsrc(qw, static_cast<uint32_t>(N) * static_cast<uint32_t>(K / 2));
-  const __amdgpu_buffer_rsrc_t sres = rsrc(scales, static_cast<uint32_t>(N) * kg * 2u);
+  // TL: the weights are in the T16 layout (q4_t16_pack): 16-row tiles in this kernel's virtual row
+  // order, 1 KB per (tile, 128-k segment), and scales [tile][4-group tile][group slot][16 rows].
+  const int nseg = n_tiles * kSegPerTile;
+  const int n_t16 = EPI == kEpiNone ? (N + 15) / 16 : ((N >> 1) + 7) / 8;
+  const __amdgpu_buffer_rsrc_t wres =
+      TL ? rsrc(qw, static_cast<uint32_t>(n_t16) * nseg * 1024u)
+         : rsrc(qw, static_cast<uint32_t>(N) * static_cast<uint32_t>(K / 2));
+  const __amdgpu_buffer_rsrc_t sres =
+      TL ? rsrc(scales, static_cast<uint32_t>(n_t16) * n_tiles * 128u) : rsrc(scales, static_cast<uint32_t>(N) * kg * 2u);
 
   // ---- weight and scale loads of one row block (this wave's tiles) ----
   // Every wave owns exactly TPW tiles (the host only picks entries with n_tiles == WPB * TPW), so
@@ -256,6 +269,32 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
   };
   const uint32_t row_bytes = static_cast<uint32_t>(K / 2);
   auto issue = [&](int rb, Regs& R) {
+    if constexpr (TL) {
+      // virtual row of this lane's weights (row c of the RPB used rows of block rb) and of its first
+      // scale row (4b); rows past the tiles read out of range (zeros, no traffic)
+      const bool live = rb < n_rb;
+      const int vr = rb * RPB + c, vs = rb * RPB + 4 * b;
+      const bool rok = live && c < RPB && (EPI != kEpiNone || vr < N);
+      const bool sok = live && 4 * b < RPB;
+      const uint32_t abase = rok ? (static_cast<uint32_t>(vr >> 4) * nseg) * 1024u + (vr & 15) * 64u + 16u * b : kOOB;
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int T = t0 + i;
+#pragma unroll
+        for (int sg = 0; sg < kSegPerTile; ++sg) {
+          const int seg = T * kSegPerTile + sg;
+          const bool ok = seg * 128 + 32 * b < K;
+          R.a[i][sg] = load16(wres, ok && abase != kOOB ? abase + 1024u * seg : kOOB);
+        }
+        const uint2 sv = load8(
+            sres, sok ? ((static_cast<uint32_t>(vs >> 4) * n_tiles + T) * 64u + q * 16u + (vs & 15)) * 2u : kOOB);
+        R.s[i][0] = static_cast<uint16_t>(sv.x);
+        R.s[i][1] = static_cast<uint16_t>(sv.x >> 16);
+        R.s[i][2] = static_cast<uint16_t>(sv.y);
+        R.s[i][3] = static_cast<uint16_t>(sv.y >> 16);
+      }
+      return;
+    }
     // byte offset of this lane's first weight chunk and of its 4 scale rows (kOOB: no such row)
     const int arow = rb < n_rb ? phys_row<EPI, RPB>(rb, c, N, ea) : -1;
     const uint32_t abase = arow >= 0 ? static_cast<uint32_t>(arow) * row_bytes + 16u * b : kOOB;
@@ -552,7 +591,7 @@ constexpr MxCfg kMxCfgs[] = {
 };
 constexpr int kNumMxCfgs = sizeof(kMxCfgs) / sizeof(kMxCfgs[0]);
 
-template <int G, int PRO, int EPI, int I>
+template <int G, int PRO, int EPI, bool TL, int I>
 constexpr MxFn mx_fn() {
   constexpr MxCfg c = kMxCfgs[I];
   if constexpr (EPI != kEpiNone && c.rpb != 16) {
@@ -560,30 +599,35 @@ constexpr MxFn mx_fn() {
   } else if constexpr (G == 32 && !(I == 0 || I == 1 || I == 2 || I == 3 || I == 17)) {
     return nullptr;  // the group-32 (tiny model) shapes use a short list
   } else {
-    return q4_gemv_mx_kernel<G, c.rbw, c.wpb, c.tpw, c.multi, PRO, EPI, c.rpb>;
+    return q4_gemv_mx_kernel<G, c.rbw, c.wpb, c.tpw, c.multi, PRO, EPI, c.rpb, TL>;
   }
 }
 
-template <int G, int PRO, int EPI, int... Is>
+template <int G, int PRO, int EPI, bool TL, int... Is>
 constexpr std::array<MxFn, sizeof...(Is)> mx_table(std::integer_sequence<int, Is...>) {
-  return {mx_fn<G, PRO, EPI, Is>()...};
+  return {mx_fn<G, PRO, EPI, TL, Is>()...};
 }
 
-template <int G, int PRO, int EPI>
+template <int G, int PRO, int EPI, bool TL>
 const std::array<MxFn, kNumMxCfgs>& mx_tab() {
-  static constexpr auto t = mx_table<G, PRO, EPI>(std::make_integer_sequence<int, kNumMxCfgs>{});
+  static constexpr auto t = mx_table<G, PRO, EPI, TL>(std::make_integer_sequence<int, kNumMxCfgs>{});
   return t;
 }
 
-template <int G>
-MxFn mx_lookup(int pro, int epi, int ci) {
-  if (pro == kProNone && epi == kEpiNone) return mx_tab<G, kProNone, kEpiNone>()[ci];
-  if (pro == kProNorm && epi == kEpiNone) return mx_tab<G, kProNorm, kEpiNone>()[ci];
-  if (pro == kProNorm && epi == kEpiSwiglu) return mx_tab<G, kProNorm, kEpiSwiglu>()[ci];
-  if (pro == kProNorm && epi == kEpiRope) return mx_tab<G, kProNorm, kEpiRope>()[ci];
-  if (pro == kProNone && epi == kEpiSwiglu) return mx_tab<G, kProNone, kEpiSwiglu>()[ci];
-  if (pro == kProNone && epi == kEpiRope) return mx_tab<G, kProNone, kEpiRope>()[ci];
+template <int G, bool TL>
+MxFn mx_lookup_tl(int pro, int epi, int ci) {
+  if (pro == kProNone && epi == kEpiNone) return mx_tab<G, kProNone, kEpiNone, TL>()[ci];
+  if (pro == kProNorm && epi == kEpiNone) return mx_tab<G, kProNorm, kEpiNone, TL>()[ci];
+  if (pro == kProNorm && epi == kEpiSwiglu) return mx_tab<G, kProNorm, kEpiSwiglu, TL>()[ci];
+  if (pro == kProNorm && epi == kEpiRope) return mx_tab<G, kProNorm, kEpiRope, TL>()[ci];
+  if (pro == kProNone && epi == kEpiSwiglu) return mx_tab<G, kProNone, kEpiSwiglu, TL>()[ci];
+  if (pro == kProNone && epi == kEpiRope) return mx_tab<G, kProNone, kEpiRope, TL>()[ci];
   return nullptr;
+}
+
+template <int G>
+MxFn mx_lookup(int pro, int epi, int ci, bool tiled) {
+  return tiled ? mx_lookup_tl<G, true>(pro, epi, ci) : mx_lookup_tl<G, false>(pro, epi, ci);
 }
 
 bool mx_fits(const MxCfg& c, int n_tiles, int nblk) {
@@ -599,7 +643,7 @@ bool mx_fits(const MxCfg& c, int n_tiles, int nblk) {
 // 4.03). Other shapes: the first fitting entry in list order (8 used rows per block when 16 give
 // fewer than 256 row blocks), grid-stride entries for matrices taller than 4096 row blocks.
 // Returns -1 when the VALU kernel should run.
-int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair) {
+int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair, bool tiled) {
   auto fits = [&](int i) { return mx_fits(kMxCfgs[i], n_tiles, nblk) && (!pair || kMxCfgs[i].rpb == 16); };
   const char* ov = getenv("Q4_MX_CFG");
   if (ov && *ov) {
@@ -608,7 +652,7 @@ int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair) {
   }
   if (n_tiles == 6 && pair) return n_rb16 <= 512 ? 11 : 8;
   if (n_tiles == 6 && !pair && n_rb16 > 4096) return 19;
-  if (n_tiles == 6 && !pair && n_rb16 == 192) return -1;
+  if (n_tiles == 6 && !pair && n_rb16 == 192 && !tiled) return -1;
   if (n_tiles == 16 && !pair && n_rb16 <= 512) return 13;
   if (!pair && n_rb16 > 4096) {
     for (int i = 0; i < kNumMxCfgs; ++i)
@@ -627,17 +671,38 @@ int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair) {
 
 }  // namespace
 
+int gemv_mx_num_cfgs() { return kNumMxCfgs; }
+
+int gemv_mx_cfg_info(int i, int* out) {
+  if (i < 0 || i >= kNumMxCfgs) return Q4_ERR_RANGE;
+  const MxCfg& c = kMxCfgs[i];
+  const int v[5] = {c.rbw, c.wpb, c.tpw, c.rpb, c.multi ? 1 : 0};
+  for (int j = 0; j < 5; ++j) out[j] = v[j];
+  return Q4_OK;
+}
+
+// Whether the matrix-core GEMV takes an (N, K, group) weight in the T16 layout (q4_t16.hip).
+bool gemv_mx_takes_t16(int64_t N, int64_t K, int group, bool pair) {
+  if (K % 32 || K > 16384 || N <= 0 || (group != 32 && group != 128) || K % group) return false;
+  if (pair && N % 2) return false;
+  const int tile_k = 4 * group;
+  const int n_tiles = static_cast<int>((K + tile_k - 1) / tile_k);
+  const int64_t n_rb16 = pair ? (N / 2 + 7) / 8 : (N + 15) / 16;
+  if (n_rb16 > (int64_t{1} << 30)) return false;
+  return mx_choose(n_tiles, n_tiles * (tile_k / 16), n_rb16, pair, true) >= 0;
+}
+
 // Launches the matrix-core GEMV; returns Q4_ERR_UNSUPPORTED (nothing launched) for shapes it does
 // not take, so the caller can use the VALU kernel. x and y fp32; prologue 0 = none, 1 = rms_norm;
 // epilogue 0 = none, 1 = SwiGLU pairs, 2 = RoPE + KV pairs (ep describes the latter).
 int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
                    const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
-                   const void* ep, hipStream_t stream) {
-  if (getenv("Q4_GEMV_NO_MX")) return Q4_ERR_UNSUPPORTED;
+                   const void* ep, hipStream_t stream, bool tiled) {
+  if (!tiled && getenv("Q4_GEMV_NO_MX")) return Q4_ERR_UNSUPPORTED;
   if (K % 32 || K > 16384 || N <= 0) return Q4_ERR_UNSUPPORTED;
   if (group != 32 && group != 128) return Q4_ERR_UNSUPPORTED;
   if (K % group) return Q4_ERR_UNSUPPORTED;
-  if (N * (K / 2) >= (int64_t{1} << 31)) return Q4_ERR_UNSUPPORTED;
+  if (!tiled && N * (K / 2) >= (int64_t{1} << 31)) return Q4_ERR_UNSUPPORTED;
   if (!aligned(qweight, 16) || !aligned(x, 16) || (aux && !aligned(aux, 16))) return Q4_ERR_UNSUPPORTED;
   if (epilogue != kEpiNone && (N % 2 || residual)) return Q4_ERR_UNSUPPORTED;
   MxEpi ea{};
@@ -651,9 +716,10 @@ int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* 
   const bool pair = epilogue != kEpiNone;
   const int64_t n_rb16 = pair ? (N / 2 + 7) / 8 : (N + 15) / 16;
   const int nblk = n_tiles * (tile_k / 16);
-  const int ci = mx_choose(n_tiles, nblk, n_rb16, pair);
+  const int ci = mx_choose(n_tiles, nblk, n_rb16, pair, tiled);
   if (ci < 0) return Q4_ERR_UNSUPPORTED;
-  const MxFn fn = group == 128 ? mx_lookup<128>(prologue, epilogue, ci) : mx_lookup<32>(prologue, epilogue, ci);
+  const MxFn fn = group == 128 ? mx_lookup<128>(prologue, epilogue, ci, tiled)
+                               : mx_lookup<32>(prologue, epilogue, ci, tiled);
   if (!fn) return Q4_ERR_UNSUPPORTED;
   const MxCfg& c = kMxCfgs[ci];
   const int64_t n_rb = pair ? n_rb16 : (N + c.rpb - 1) / c.rpb;
@@ -678,3 +744,9 @@ int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* 
 }
 
 }  // namespace q4
+
+extern "C" int q4_gemv_mx_num_configs(void) { return q4::gemv_mx_num_cfgs(); }
+extern "C" int q4_gemv_mx_config_info(int cfg, int* info) {
+  if (!info) return Q4_ERR_NULL;
+  return q4::gemv_mx_cfg_info(cfg, info);
+}

@@ -680,6 +680,14 @@ int q4_linear_launch(const float* x, int64_t M, const int32_t* qw, const uint16_
 
 int q4_linear_ws_num_tiles() { return kNumLinWs; }
 
+int q4_linear_ws_tile_info(int i, int* out) {
+  if (i < 0 || i >= kNumLinWs) return Q4_ERR_RANGE;
+  const LinWsTile& t = kLinWsTiles[i];
+  const int v[6] = {t.bm, t.bn, t.wm, t.wn, t.nst, t.ks};
+  for (int j = 0; j < 6; ++j) out[j] = v[j];
+  return Q4_OK;
+}
+
 namespace {
 // What the pipelined GEMM's index arithmetic assumes: every 64-k stage lies in whole groups of a
 // power of two >= 32 (at most two scale slots per stage, groups found by shifts), K a multiple of
@@ -781,6 +789,11 @@ int linear_args(const float* x, int64_t M, const int32_t* qweight, const uint16_
 }  // namespace
 
 extern "C" int q4_linear_ws_num_configs(void) { return q4::q4_linear_ws_num_tiles(); }
+
+extern "C" int q4_linear_ws_config_info(int cfg, int* info) {
+  if (!info) return Q4_ERR_NULL;
+  return q4::q4_linear_ws_tile_info(cfg, info);
+}
 
 extern "C" int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes) {
   if (!bytes) return Q4_ERR_NULL;

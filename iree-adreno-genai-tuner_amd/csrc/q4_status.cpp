@@ -31,4 +31,4 @@ extern "C" const char* q4llm_status_string(int status) {
 
 extern "C" int q4llm_last_hip_error(void) { return q4::g_last_hip_error; }
 
-extern "C" int q4llm_abi_version(void) { return 1; }
+extern "C" int q4llm_abi_version(void) { return 2; }

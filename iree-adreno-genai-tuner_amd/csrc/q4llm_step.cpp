@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
+#include <cstdlib>
 #include <mutex>
 
 #include "q4_common.h"
@@ -171,6 +172,9 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
   uint16_t* xh = static_cast<uint16_t*>(lin_ws);
   uint16_t* xl = xh + static_cast<size_t>(C) * kmax;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  // decode GEMVs on the T16 copies where the model has them (Q4_NO_T16 set: the reference layout)
+  const bool use_t16 = fused && !getenv("Q4_NO_T16");
+  auto has = [&](const q4llm_t16& t) { return use_t16 && t.tiles && t.scales; };
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
@@ -178,8 +182,12 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
     uint16_t* vc = static_cast<uint16_t*>(caches[2 * i + 1]);
     if (fused) {
       const q4_rope_kv rope{m->cos_t, m->sin_t, kc, vc, start, nh, nkv, hd, m->max_ctx};
-      Q4_TRY(q4_gemv_epilogue(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV, &rope, qkv,
-                              qkv_w, D, m->group, stream));
+      if (has(ly.wqkv_t))
+        Q4_TRY(q4_gemv_t16(ly.wqkv_t.tiles, ly.wqkv_t.scales, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV,
+                           &rope, qkv, nullptr, qkv_w, D, m->group, stream));
+      else
+        Q4_TRY(q4_gemv_epilogue(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV, &rope, qkv,
+                                qkv_w, D, m->group, stream));
     } else if (planes) {
       Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st));
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st));
@@ -195,12 +203,24 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st));
     } else {
       Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
-      Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, lin_ws, lo.lin_bytes, stream));
+      if (has(ly.wo_t))
+        Q4_TRY(q4_gemv_t16(ly.wo_t.tiles, ly.wo_t.scales, o, Q4_PRO_NONE, nullptr, 0.0f, 0, nullptr, h, h, D, nq_w,
+                           m->group, stream));
+      else
+        Q4_TRY(proj(C, o, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, lin_ws, lo.lin_bytes, stream));
     }
     if (fused) {
-      Q4_TRY(q4_gemv_epilogue(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU, nullptr, act,
-                              2 * m->inter, D, m->group, stream));
-      Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
+      if (has(ly.wgu_t))
+        Q4_TRY(q4_gemv_t16(ly.wgu_t.tiles, ly.wgu_t.scales, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU,
+                           nullptr, act, nullptr, 2 * m->inter, D, m->group, stream));
+      else
+        Q4_TRY(q4_gemv_epilogue(ly.wgu_q, ly.wgu_s, h, Q4_PRO_RMSNORM, ly.ln_post, m->eps, Q4_EPI_SWIGLU, nullptr, act,
+                                2 * m->inter, D, m->group, stream));
+      if (has(ly.wdown_t))
+        Q4_TRY(q4_gemv_t16(ly.wdown_t.tiles, ly.wdown_t.scales, act, Q4_PRO_NONE, nullptr, 0.0f, 0, nullptr, h, h, D,
+                           m->inter, m->group, stream));
+      else
+        Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
     } else if (planes) {
       Q4_TRY(q4::rmsnorm_planes(h, ly.ln_post, xh, xl, C, D, m->eps, st));
       // gate/up + SwiGLU in one kernel where the shape takes it (its planes go to the gu buffer, which
@@ -224,8 +244,12 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
     }
   }
   if (fused) {  // one row: the final norm is the LM head's prologue
-    Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
-                         m->group, stream));
+    if (has(m->embed_t))
+      Q4_TRY(q4_gemv_t16(m->embed_t.tiles, m->embed_t.scales, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, 0, nullptr, lg,
+                         nullptr, m->vocab, D, m->group, stream));
+    else
+      Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
+                           m->group, stream));
   } else {
     Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
     Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));

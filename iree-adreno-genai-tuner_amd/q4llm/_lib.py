@@ -35,6 +35,9 @@ SIGNATURES = {
     "q4_gemv_num_configs": [],
     "q4_gemv_fused": [p, p, p, i32, p, f32, p, p, i64, i64, i32, p],
     "q4_gemv_epilogue": [p, p, p, i32, p, f32, i32, p, p, i64, i64, i32, p],
+    "q4_t16_bytes": [i64, i64, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)],
+    "q4_t16_pack": [p, p, i64, i64, i32, i32, i32, p, p, p],
+    "q4_gemv_t16": [p, p, p, i32, p, f32, i32, p, p, p, i64, i64, i32, p],
     "q4_linear": [p, i64, p, p, p, p, i64, i64, i32, p],
     "q4_linear_workspace_bytes": [i64, i64, C.POINTER(sz)],
     "q4_linear_ws": [p, i64, p, p, p, p, i64, i64, i32, p, sz, p],
@@ -42,6 +45,11 @@ SIGNATURES = {
     "gemm_f16_nt_cfg": [p, p, p, i64, i64, i64, i64, i64, i64, i32, i32, p],
     "gemm_f16_num_configs": [],
     "q4_linear_ws_num_configs": [],
+    "q4_gemv_config_info": [i32, p],
+    "q4_gemv_mx_num_configs": [],
+    "q4_gemv_mx_config_info": [i32, p],
+    "gemm_f16_config_info": [i32, p],
+    "q4_linear_ws_config_info": [i32, p],
     "attn_workspace_bytes": [i32, i32, i32, i32, i32, C.POINTER(sz)],
     "attn_bucket": [p, i32, p, p, p, i32, i32, i32, i32, i32, p, f32, p, sz, p],
     "rmsnorm_f32": [p, p, p, i64, i64, f32, p, p],
@@ -127,3 +135,14 @@ def stream_of(device=None) -> int:
     import torch
     return torch.cuda.current_stream(device).cuda_stream
 
+
+def config_table(kind: str):
+    """Entries of one of the library's explicit tile lists as tuples (see include/q4llm.h):
+    'gemv', 'gemv_mx', 'gemm' or 'linear_ws'."""
+    fn, width = {"gemv": ("q4_gemv_config_info", 6), "gemv_mx": ("q4_gemv_mx_config_info", 5),
+                 "gemm": ("gemm_f16_config_info", 7), "linear_ws": ("q4_linear_ws_config_info", 6)}[kind]
+    out = []
+    buf = (C.c_int * 8)()
+    while LIB.raw(fn)(len(out), buf) == Q4_OK:
+        out.append(tuple(buf[:width]))
+    return out

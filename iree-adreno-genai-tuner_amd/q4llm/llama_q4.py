@@ -166,15 +166,26 @@ class Layer(nn.Module):
         self.ln_post = nn.Parameter(dev("post_attention_layernorm.weight").contiguous(), requires_grad=False)
 
 
+class _T16C(C.Structure):
+    _fields_ = [("tiles", C.c_void_p), ("scales", C.c_void_p)]
+
+
 class _LayerC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("wqkv_q", "wqkv_s", "wo_q", "wo_s", "wgu_q", "wgu_s", "wdown_q",
-                                          "wdown_s", "ln_in", "ln_post")]
+                                          "wdown_s", "ln_in", "ln_post")] + \
+               [(n, _T16C) for n in ("wqkv_t", "wo_t", "wgu_t", "wdown_t")]
 
 
 class _ModelC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("dim", "n_layers", "n_heads", "n_kv", "head_dim", "inter", "vocab", "group",
                                        "max_ctx")] + [("eps", C.c_float)] + \
-               [(n, C.c_void_p) for n in ("embed_q", "embed_s", "ln_f", "cos_t", "sin_t", "layers")]
+               [(n, C.c_void_p) for n in ("embed_q", "embed_s", "ln_f", "cos_t", "sin_t", "layers")] + \
+               [("embed_t", _T16C)]
+
+
+# Decode projections that get a T16 copy, with the pairing their GEMV epilogue needs. The o-projection
+# keeps the reference layout: its VALU GEMV is as fast as the matrix-core one on T16 at 3072x3072.
+_T16_ROLES = {"wqkv": ops.PAIR_ROPE, "wgu": ops.PAIR_SWIGLU, "wdown": ops.PAIR_NONE}
 
 
 class LlamaQ4(nn.Module):
@@ -211,10 +222,29 @@ class LlamaQ4(nn.Module):
     def _finish(self, cos, sin):
         self.register_buffer("cos", cos.to(self.device).contiguous(), persistent=False)
         self.register_buffer("sin", sin.to(self.device).contiguous(), persistent=False)
+        self._build_t16()
         self._desc = None
         self._ws = {}
         self._io = None
         self._graphs = {}
+
+    def _build_t16(self):
+        """T16 copies of the decode projections and the LM head (include/q4llm.h), built on the device
+        from the reference-layout weights; shapes the decode GEMV does not take keep no copy."""
+        self.t16 = {}
+        for i, ly in enumerate(self.layers):
+            for nm, pairing in _T16_ROLES.items():
+                q = getattr(ly, nm)
+                t = ops.t16_pack(q.qweight, q.scales, self.group, pairing, self.head_dim)
+                if t is not None:
+                    self.t16[(i, nm)] = t
+        t = ops.t16_pack(self.embed.qweight, self.embed.scales, self.group)
+        if t is not None:
+            self.t16["embed"] = t
+
+    def _t16c(self, key):
+        t = self.t16.get(key)
+        return _T16C(ptr(t[0]), ptr(t[1])) if t is not None else _T16C(None, None)
 
     # ---------------------------------------------------------------- packed weights
 
@@ -288,10 +318,11 @@ class LlamaQ4(nn.Module):
             for i, ly in enumerate(self.layers):
                 arr[i] = _LayerC(ptr(ly.wqkv.qweight), ptr(ly.wqkv.scales), ptr(ly.wo.qweight), ptr(ly.wo.scales),
                                  ptr(ly.wgu.qweight), ptr(ly.wgu.scales), ptr(ly.wdown.qweight),
-                                 ptr(ly.wdown.scales), ptr(ly.ln_in), ptr(ly.ln_post))
+                                 ptr(ly.wdown.scales), ptr(ly.ln_in), ptr(ly.ln_post), self._t16c((i, "wqkv")),
+                                 self._t16c((i, "wo")), self._t16c((i, "wgu")), self._t16c((i, "wdown")))
             m = _ModelC(self.dim, self.n_layers, self.n_heads, self.n_kv, self.head_dim, self.inter, self.embed.vocab,
                         self.group, self.max_ctx, self.eps, ptr(self.embed.qweight), ptr(self.embed.scales),
-                        ptr(self.ln_f), ptr(self.cos), ptr(self.sin), C.cast(arr, C.c_void_p))
+                        ptr(self.ln_f), ptr(self.cos), ptr(self.sin), C.cast(arr, C.c_void_p), self._t16c("embed"))
             self._desc = (m, arr)
         return self._desc[0]
 

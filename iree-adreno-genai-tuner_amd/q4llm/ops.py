@@ -287,3 +287,48 @@ def argmax(logits, out=None, workspace=None):
     LIB.call("argmax_f32", ptr(logits), v, ptr(out), ptr(workspace), workspace.numel(),
              stream_of(logits.device))
     return out
+
+
+PAIR_NONE, PAIR_SWIGLU, PAIR_ROPE = 0, 1, 2
+
+
+def t16_bytes(N, K, group, pairing=PAIR_NONE, head_dim=0):
+    """(tile bytes, scale bytes) of the T16 copy, or None when the decode GEMV does not take the shape."""
+    tb, sb = C.c_size_t(0), C.c_size_t(0)
+    st = LIB.raw("q4_t16_bytes")(N, K, group, pairing, head_dim, C.byref(tb), C.byref(sb))
+    if st == -7:  # Q4_ERR_UNSUPPORTED
+        return None
+    if st != 0:
+        LIB.call("q4_t16_bytes", N, K, group, pairing, head_dim, C.byref(tb), C.byref(sb))
+    return tb.value, sb.value
+
+
+def t16_pack(qweight, scales, group, pairing=PAIR_NONE, head_dim=0):
+    """The T16 device copy (tiles uint8, tile scales fp16) of an int4 weight, or None if unsupported."""
+    n, k = _weights(qweight, scales, group)
+    _dev(qweight, scales)
+    sz = t16_bytes(n, k, group, pairing, head_dim)
+    if sz is None:
+        return None
+    tiles = torch.empty(sz[0], dtype=torch.uint8, device=qweight.device)
+    tsc = torch.empty(sz[1] // 2, dtype=torch.float16, device=qweight.device)
+    LIB.call("q4_t16_pack", ptr(qweight), ptr(scales), n, k, group, pairing, head_dim, ptr(tiles), ptr(tsc),
+             stream_of(qweight.device))
+    return tiles, tsc
+
+
+def q4_gemv_t16(tiles, tile_scales, x, N, K, group, norm_w=None, eps=1e-5, epilogue=0, rope=None, residual=None,
+                out=None):
+    """Decode GEMV on a T16 copy (fp32 x, y): y = residual + W x' with x' = rms_norm(x, norm_w, eps) when
+    norm_w is given; epilogue EPI_SWIGLU / EPI_ROPE_KV as q4_gemv_swiglu / q4_gemv_rope_kv (rope: RopeKV)."""
+    x = x.reshape(-1).contiguous()
+    _need(x, "x", torch.float32, (K,))
+    _need(residual, "residual", torch.float32, (N,))
+    _dev(tiles, tile_scales, x, norm_w, residual, out)
+    if out is None:
+        n_out = N // 2 if epilogue == EPI_SWIGLU else N
+        out = torch.empty(n_out, dtype=torch.float32, device=x.device)
+    pro = PRO_RMSNORM if norm_w is not None else PRO_NONE
+    LIB.call("q4_gemv_t16", ptr(tiles), ptr(tile_scales), ptr(x), pro, ptr(norm_w), eps, epilogue,
+             None if rope is None else C.addressof(rope), ptr(out), ptr(residual), N, K, group, stream_of(x.device))
+    return out

@@ -19,7 +19,7 @@ def test_library_loads_and_exports_header():
     assert len(names) >= 25
     missing = [n for n in names if getattr(dll, n, None) is None]
     assert not missing, missing
-    assert dll.q4llm_abi_version() == 1
+    assert dll.q4llm_abi_version() == 2
 
 
 def test_status_strings():
