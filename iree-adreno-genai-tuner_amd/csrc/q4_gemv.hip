@@ -55,8 +55,9 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// fp16 scales: streamed once per launch like the weights (nontemporal)
 __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 2);
 }
 
 template <bool kF16X>

@@ -60,13 +60,18 @@ __device__ __forceinline__ i32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+// Weight stream: read once per launch, marked nontemporal (cache policy bit 1).
+__device__ __forceinline__ i32x4 load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+}
+
 __device__ __forceinline__ uint16_t load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 2);
 }
 
 __device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-  const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2);
   return make_uint2(static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y));
 }
 
@@ -284,7 +289,7 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
         for (int sg = 0; sg < kSegPerTile; ++sg) {
           const int seg = T * kSegPerTile + sg;
           const bool ok = seg * 128 + 32 * b < K;
-          R.a[i][sg] = load16(wres, ok && abase != kOOB ? abase + 1024u * seg : kOOB);
+          R.a[i][sg] = load16_nt(wres, ok && abase != kOOB ? abase + 1024u * seg : kOOB);
         }
         const uint2 sv = load8(
             sres, sok ? ((static_cast<uint32_t>(vs >> 4) * n_tiles + T) * 64u + q * 16u + (vs & 15)) * 2u : kOOB);
@@ -311,7 +316,7 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
       for (int sg = 0; sg < kSegPerTile; ++sg) {
         const int seg = T * kSegPerTile + sg;
         const bool ok = seg * 128 + 32 * b < K;
-        R.a[i][sg] = load16(wres, ok ? abase + 64u * seg : kOOB);
+        R.a[i][sg] = load16_nt(wres, ok ? abase + 64u * seg : kOOB);
       }
       const bool gok = 4 * T + q < kg;
 #pragma unroll
