@@ -1,0 +1,413 @@
+"""Host-side replay of the kernels' index mapping for every entry of the explicit tile lists (the
+analogue of the reference's gemm/verifier.py mapping_check, :135-176): at ragged shapes, each output
+is written exactly once, each weight chunk / k step is read and reduced exactly once, and every load
+either lands inside its buffer at the element it stands for or is a deliberate out-of-range offset
+(answered with zeros by the buffer resource) that cannot wrap the 32-bit offset. The entries come
+from the library (q4_gemv_config_info, q4_gemv_mx_config_info, gemm_f16_config_info,
+q4_linear_ws_config_info); the index formulas restate the kernels (file:function cited per test).
+No GPU is needed."""
+
+import numpy as np
+import pytest
+
+from q4llm._lib import config_table
+
+OOB = 0x80000000
+
+
+def cdiv(a, b):
+    return -(-a // b)
+
+
+# ------------------------------------------------------------------------------------------------
+# VALU decode GEMV (csrc/q4_gemv.hip: q4_gemv_kernel, load_item / compute_item / stage_store)
+# ------------------------------------------------------------------------------------------------
+
+def gemv_fits(cfg, N, K):
+    lpr, cpl, r, waves, xw, multi = cfg
+    cpr = K // 32
+    if K // 8 > xw * 64 * waves:
+        return False
+    if not multi and lpr * cpl < cpr:
+        return False
+    return True
+
+
+def replay_gemv(cfg, N, K, gshift, paired):
+    lpr, cpl, R, waves, xw, multi = cfg
+    cpr, spr, nwords = K // 32, (K // 32) >> gshift, K // 8
+    rows_per_wave = R * (64 // lpr)
+    rows_wg = rows_per_wave * waves
+    n_blocks = cdiv(N, rows_wg)
+    grid = min(n_blocks, 1024) if multi else n_blocks
+    n_kpass = cdiv(cpr, lpr * cpl) if multi else 1
+    wbytes, sbytes = N * (K // 2), N * spr * 2
+    reads = np.zeros((N, cpr), np.int32)
+    sreads = np.zeros((N, spr), np.int32)
+    stores = np.zeros(N if not paired else N // 2, np.int32)
+
+    def phys(v):
+        if not paired:
+            return v
+        pr, b = v >> 1, v & 1
+        return N if pr >= N // 2 else pr + b * (N // 2)  # SwiGLU pairing
+
+    lane = np.arange(64)
+    lr, rg = lane % lpr, lane // lpr
+    for blk in range(grid):
+        my = cdiv(n_blocks - blk, grid) if blk < n_blocks else 0
+        n_items = my * n_kpass if multi else 1
+        # grid-stride loops run items in pairs (it, it + 1); the odd tail item is past the end
+        items = range(n_items + (n_items % 2) if multi else 1)
+        for wave in range(waves):
+            for it in items:
+                kp = it % n_kpass
+                row0 = (blk + (it // n_kpass) * grid) * rows_wg + wave * rows_per_wave + rg * R
+                for rr in range(R):
+                    v = row0 + rr
+                    row = np.array([phys(int(x)) for x in v])
+                    for i in range(cpl):
+                        c = kp * (lpr * cpl) + i * lpr + lr
+                        woff = np.where(c < cpr, row.astype(np.int64) * (K // 2) + c * 16, OOB)
+                        soff = np.where(c < cpr, (row.astype(np.int64) * spr + (c >> gshift)) * 2, OOB)
+                        assert (woff < 2 ** 32).all() and (soff < 2 ** 32).all(), "offset wraps"
+                        live = (woff < wbytes) & (c < cpr)
+                        assert ((woff >= wbytes) | live).all()
+                        np.add.at(reads, (row[live], c[live]), 1)
+                        sl = soff < sbytes
+                        np.add.at(sreads, (row[sl], (c[sl] >> gshift)), 1)
+                if kp == n_kpass - 1:
+                    last = lr == lpr - 1
+                    if paired:
+                        pr = (row0[last] >> 1)
+                        np.add.at(stores, pr[pr < N // 2], 1)
+                    else:
+                        for rr in range(R):
+                            rows = (row0 + rr)[last]
+                            np.add.at(stores, rows[rows < N], 1)
+    assert (reads == 1).all(), "weight chunks read other than once"
+    assert (sreads == 1 << gshift).all(), "each scale feeds its group's chunks"
+    assert (stores == 1).all(), "outputs stored other than once"
+    # x staging: word wd = thread + i * threads, i < xw, each word of K staged once
+    thr = np.arange(64 * waves)
+    wd = (thr[None, :] + np.arange(xw)[:, None] * 64 * waves).ravel()
+    staged = np.bincount(wd[wd < nwords], minlength=nwords)
+    assert (staged == 1).all()
+
+
+@pytest.mark.parametrize("idx", range(len(config_table("gemv"))))
+def test_gemv_entries_cover_once(idx):
+    cfg = config_table("gemv")[idx]
+    lpr, cpl, r, waves, xw, multi = cfg
+    ran = 0
+    for K in (256, 704, 1024, 3072, 4096, 8192):
+        for N in (40, 1000, 3 * 64 * waves + 7):
+            if not gemv_fits(cfg, N, K) or (multi and N > 2000):
+                continue
+            for gshift in (0, 2):
+                if (K // 32) % (1 << gshift):
+                    continue
+                replay_gemv(cfg, N, K, gshift, False)
+                if r == 2 and not multi:
+                    replay_gemv(cfg, N - N % 2, K, gshift, True)
+                ran += 1
+            break
+    assert ran > 0
+
+
+# ------------------------------------------------------------------------------------------------
+# Matrix-core decode GEMV (csrc/q4_gemv_mx.hip: q4_gemv_mx_kernel issue / compute, both layouts)
+# ------------------------------------------------------------------------------------------------
+
+def mx_fits(cfg, n_tiles, nblk):
+    rbw, wpb, tpw, rpb, multi = cfg
+    return n_tiles == wpb * tpw and 64 * rbw * wpb >= nblk
+
+
+def replay_mx(cfg, N, K, G, pair, tiled):
+    rbw, wpb, tpw, rpb, multi = cfg
+    seg_per_tile = 4 * G // 128
+    n_tiles = cdiv(K, 4 * G)
+    nseg = n_tiles * seg_per_tile
+    kg = K // G
+    n_rb = cdiv(N // 2, 8) if pair else cdiv(N, rpb)
+    n_t16 = cdiv(N // 2, 8) if pair else cdiv(N, 16)
+    wbytes = n_t16 * nseg * 1024 if tiled else N * (K // 2)
+    n_wg = cdiv(n_rb, rbw)
+    grid = min(n_wg, 1024) if multi else n_wg
+    reads = np.zeros((N, cdiv(K, 32)), np.int32)
+    stores = np.zeros(N // 2 if pair else N, np.int32)
+
+    def phys(rb, v):  # q4_gemv_mx.hip phys_row (SwiGLU pairing for pair=True)
+        if not pair:
+            r = rb * rpb + v
+            return r if (v < rpb and r < N) else -1
+        p = rb * 8 + (v & 7)
+        if p >= N // 2:
+            return -1
+        return p + (N // 2 if v >= 8 else 0)
+
+    lane = np.arange(64)
+    c, b = lane & 15, lane >> 4
+    for wg0 in range(grid):
+        my = cdiv(n_wg - wg0, grid) if wg0 < n_wg else 0
+        wgs = [wg0 + it * grid for it in range(my)] if multi else [wg0]
+        for wg in wgs:
+            for wave in range(rbw * wpb):
+                rbl, wp = wave // wpb, wave % wpb
+                rb = wg * rbw + rbl
+                for i in range(tpw):
+                    T = wp * tpw + i
+                    for sg in range(seg_per_tile):
+                        seg = T * seg_per_tile + sg
+                        for ln in range(64):
+                            if rb >= n_rb:
+                                continue
+                            k0 = seg * 128 + 32 * b[ln]
+                            row = phys(rb, c[ln])
+                            if tiled:
+                                vr = rb * rpb + c[ln] if not pair else rb * 16 + c[ln]
+                                ok = rb < n_rb and c[ln] < rpb and (pair or vr < N) and k0 < K
+                                off = ((vr >> 4) * nseg + seg) * 1024 + (vr & 15) * 64 + 16 * b[ln] if ok else OOB
+                            else:
+                                ok = row >= 0 and k0 < K
+                                off = row * (K // 2) + 64 * seg + 16 * b[ln] if ok else OOB
+                            assert off < 2 ** 32
+                            if off < wbytes and row >= 0 and k0 < K:
+                                if not tiled:
+                                    assert off == row * (K // 2) + k0 // 2
+                                reads[row, k0 // 32] += 1
+            # epilogue: thread tid < 16 RBW finishes virtual row tid % 16 of block tid / 16
+            for tid in range(16 * rbw):
+                rb, v = wg * rbw + tid // 16, tid % 16
+                if rb >= n_rb:
+                    continue
+                if pair:
+                    p = rb * 8 + v
+                    if v < 8 and p < N // 2:
+                        stores[p] += 1
+                else:
+                    row = rb * rpb + v
+                    if v < rpb and row < N:
+                        stores[row] += 1
+    assert (reads == 1).all(), "weight chunks read other than once"
+    assert (stores == 1).all(), "outputs stored other than once"
+    # x prologue: thread tid owns 16-k block tid (< nblk)
+    assert 64 * rbw * wpb >= n_tiles * (4 * G // 16)
+
+
+@pytest.mark.parametrize("idx", range(len(config_table("gemv_mx"))))
+def test_mx_entries_cover_once(idx):
+    cfg = config_table("gemv_mx")[idx]
+    rbw, wpb, tpw, rpb, multi = cfg
+    ran = 0
+    for G, K in ((128, 3072), (128, 8192), (32, 256), (32, 704)):
+        n_tiles = cdiv(K, 4 * G)
+        if not mx_fits(cfg, n_tiles, n_tiles * 4 * G // 16):
+            continue
+        if G == 32 and idx not in (0, 1, 2, 3, 17):
+            continue
+        for N in (48, 250):
+            for tiled in (False, True):
+                replay_mx(cfg, N, K, G, False, tiled)
+                if rpb == 16:
+                    replay_mx(cfg, N, K, G, True, tiled)
+                ran += 1
+        break
+    assert ran > 0
+
+
+# ------------------------------------------------------------------------------------------------
+# fp16 GEMM (csrc/gemm_f16.hip: gemm_f16_nt_kernel / gemm_f16_nt_pp_kernel)
+# ------------------------------------------------------------------------------------------------
+
+def swz(bk, r):
+    return (r >> 1) & 7 if bk == 64 else (r >> 2) & 3
+
+
+def tile_of(bid, tiles_m, tiles_n, remap):
+    ntiles = tiles_m * tiles_n
+    if remap:
+        bid = (bid % 8) * (ntiles // 8) + bid // 8
+    group = bid // (4 * tiles_n)
+    first_m = group * 4
+    gsize = min(tiles_m - first_m, 4)
+    in_group = bid - group * 4 * tiles_n
+    return first_m + in_group % gsize, in_group // gsize
+
+
+def replay_gemm(cfg, M, N, K):
+    bm, bn, wm, wn, nst, bk, pp = cfg
+    waves = wm * wn
+    row_b = bk * 2
+    rows_per_inst = 1024 // row_b
+    kcpr = bk // 8
+    kai = cdiv(bm // rows_per_inst, waves)
+    kbi = cdiv(bn // rows_per_inst, waves)
+    tiles_m, tiles_n = cdiv(M, bm), cdiv(N, bn)
+    ntiles = tiles_m * tiles_n
+    remap = 1 if ntiles % 8 == 0 else 0
+    seen = np.zeros((tiles_m, tiles_n), np.int32)
+    for bid in range(ntiles):
+        tm, tn = tile_of(bid, tiles_m, tiles_n, remap)
+        seen[tm, tn] += 1
+    assert (seen == 1).all(), "tile order is not a permutation"
+    lane = np.arange(64)
+    lda = ldb = K
+    abytes, bbytes = (M - 1) * lda * 2 + K * 2, (N - 1) * ldb * 2 + K * 2
+    # one stage of one tile (m0 = n0 = 0 covers the in-range rows; a ragged last tile below)
+    for (m0, n0) in ((0, 0), ((tiles_m - 1) * bm, (tiles_n - 1) * bn)):
+        for nrows, base, nbytes, ld, ni, limit in ((bm, m0, abytes, lda, kai, M), (bn, n0, bbytes, ldb, kbi, N)):
+            filled = np.zeros((nrows, kcpr), np.int32)
+            for k0 in range(0, K, bk):
+                filled[:] = 0
+                for wave in range(waves):
+                    for j in range(ni):
+                        blk = wave + j * waves
+                        r = blk * rows_per_inst + lane // kcpr
+                        real = blk < nrows // rows_per_inst
+                        if not pp:
+                            assert real or j >= 1 or blk < nrows // rows_per_inst
+                        elif not real:
+                            pytest.fail("ping-pong loads must divide evenly")
+                        if not real:
+                            continue  # spare instructions land in the junk area
+                        chunk = (lane % kcpr) ^ swz(bk, r)
+                        for ln in range(64):
+                            slot = ln % kcpr
+                            g_row, g_k = base + r[ln], k0 + 8 * chunk[ln]
+                            in_range = g_row < limit and g_k < K
+                            off = (g_row * ld * 2 + chunk[ln] * 16 + k0 * 2) if in_range else OOB
+                            assert off < 2 ** 31 or off == OOB
+                            if in_range:
+                                assert off < nbytes
+                            filled[r[ln], slot] += 1
+                            # the reader of (row, chunk c) looks at slot c ^ swz(row): it holds chunk c
+                            assert (slot ^ swz(bk, r[ln])) == chunk[ln]
+                assert (filled == 1).all(), "LDS stage slots filled other than once"
+                break  # the pattern is the same for every k step; K raggedness is the g_k < K test
+    # operand reads: lane supplies row lane % 32 and chunk 2 kk + lane / 32 of each 16-k step
+    ks = np.zeros(bk // 8, np.int32)
+    for kk in range(bk // 16):
+        for ln in range(64):
+            ks[2 * kk + ln // 32] += 1
+    assert (ks == 32).all()
+    # epilogue: (i, j, e, lane) -> (row, col) covers the tile once
+    wtm, wtn = bm // wm, bn // wn
+    out = np.zeros((bm, bn), np.int32)
+    for wave in range(waves):
+        wmi, wni = wave // wn, wave % wn
+        for i in range(wtm // 32):
+            for j in range(wtn // 32):
+                for e in range(16):
+                    row = wmi * wtm + i * 32 + 8 * (e // 4) + 4 * (lane >> 5) + (e % 4)
+                    col = wni * wtn + j * 32 + (lane & 31)
+                    np.add.at(out, (row, col), 1)
+    assert (out == 1).all(), "tile outputs stored other than once"
+
+
+@pytest.mark.parametrize("idx", range(len(config_table("gemm"))))
+def test_gemm_entries_cover_once(idx):
+    cfg = config_table("gemm")[idx]
+    for (M, N, K) in ((300, 520, 200), (cfg[0] * 2, cfg[1] * 4, 512)):
+        replay_gemm(cfg, M, N, K)
+
+
+# ------------------------------------------------------------------------------------------------
+# W4A16 prefill GEMM (csrc/q4_linear.hip: q4_linear_ws_kernel)
+# ------------------------------------------------------------------------------------------------
+
+def replay_linear_ws(cfg, M, N, K, group):
+    bm, bn, wm, wn, nst, ks_n = cfg
+    waves = wm * wn * ks_n
+    kai = cdiv(bm // 8, waves)
+    kbi = cdiv(bn // 32, waves)
+    gshift = group.bit_length() - 1
+    spr = K >> gshift
+    tiles_n = cdiv(N, bn)
+    tiles = cdiv(M, bm) * tiles_n
+    seen = np.zeros(tiles, np.int32)
+    lane = np.arange(64)
+    for blk in range(tiles):
+        seen[(blk // tiles_n) * tiles_n + blk % tiles_n] += 1
+    assert (seen == 1).all()
+    # x planes: rows 8b..8b+7 per instruction, slot lane % 8 of row 8b + lane / 8 holds chunk slot ^ ((r >> 1) & 7)
+    xfill = np.zeros((bm, 8), np.int32)
+    for wave in range(waves):
+        for j in range(kai):
+            b = wave + j * waves
+            if b >= bm // 8:
+                continue
+            r = 8 * b + (lane >> 3)
+            chunk = (lane & 7) ^ ((r >> 1) & 7)
+            np.add.at(xfill, (r, lane & 7), 1)
+            # the reader of chunk c of row r (c ^ ((r >> 1) & 7) slot) finds chunk c
+            assert (((lane & 7) ^ ((r >> 1) & 7)) == chunk).all()
+    assert (xfill == 1).all()
+    # weights: rows 32b + lane / 2, 16-byte half lane % 2 of the 32-byte (64-nibble) step row
+    wfill = np.zeros((bn, 2), np.int32)
+    for wave in range(waves):
+        for j in range(kbi):
+            b = wave + j * waves
+            if b >= bn // 32:
+                continue
+            np.add.at(wfill, (32 * b + (lane >> 1), lane & 1), 1)
+    assert (wfill == 1).all()
+    # k split: 16-k step kk of each 64-k stage belongs to wave group kk // (4 / KS); every step once
+    kk_owner = np.zeros(4, np.int32)
+    for ksi in range(ks_n):
+        for q in range(4 // ks_n):
+            kk_owner[ksi * (4 // ks_n) + q] += 1
+    assert (kk_owner == 1).all()
+    # group scales: applied once per group at its last 16-k step (or, k-split, per wave part)
+    applied = np.zeros((K >> gshift), np.int32)
+    for k0 in range(0, K, 64):
+        for ksi in range(ks_n):
+            for q in range(4 // ks_n):
+                kk = ksi * (4 // ks_n) + q
+                k = k0 + 16 * kk
+                ends_here = ((k + 16) & (group - 1)) == 0
+                ends_in_stage = ks_n > 1 and q == 4 // ks_n - 1 and ((((k >> gshift) + 1) << gshift) <= k0 + 64)
+                if ends_here or ends_in_stage:
+                    applied[k >> gshift] += 1
+                    # the scale slot used must be one of the stage's two groups
+                    assert (k >> gshift) - (k0 >> gshift) in (0, 1)
+    per_group = ks_n if group < 64 else 1
+    assert (applied >= 1).all()
+    if ks_n == 1:
+        assert (applied == 1).all()
+    # epilogue: each tile output once
+    wtm, wtn = bm // wm, bn // wn
+    out = np.zeros((bm, bn), np.int32)
+    for wt in range(wm * wn):
+        wmi, wni = wt // wn, wt % wn
+        for i in range(wtm // 32):
+            for j in range(wtn // 32):
+                for e in range(16):
+                    row = wmi * wtm + i * 32 + 8 * (e // 4) + 4 * (lane >> 5) + (e % 4)
+                    col = wni * wtn + j * 32 + (lane & 31)
+                    np.add.at(out, (row, col), 1)
+    assert (out == 1).all()
+    del per_group
+
+
+@pytest.mark.parametrize("idx", range(len(config_table("linear_ws"))))
+def test_linear_ws_entries_cover_once(idx):
+    cfg = config_table("linear_ws")[idx]
+    for group in (32, 128):
+        replay_linear_ws(cfg, 100, 3 * cfg[1] + 32, 512, group)
+
+
+@pytest.mark.parametrize("bk", [64, 32])
+def test_gemm_swizzle_is_bank_conflict_free(bk):
+    """An MFMA operand read takes 16 consecutive tile rows at one 16-byte chunk; gfx950's LDS serves
+    16 lanes x 16 bytes per clock from 16 groups of 16 bytes, so the 16 addresses must fall in 16
+    distinct groups (csrc/gemm_f16.hip swz)."""
+    row_b = bk * 2
+    for c in range(bk // 8):
+        for r0 in range(0, 256, 16):
+            groups = {((r * row_b + ((c ^ swz(bk, r)) << 4)) // 16) % 16 for r in range(r0, r0 + 16)}
+            assert len(groups) == 16, (c, r0)
+    # and the identity mapping (no swizzle) would not be: the check discriminates
+    groups = {((r * row_b) // 16) % 16 for r in range(16)}
+    assert len(groups) < 16
