@@ -77,7 +77,7 @@ def timed_steps(fn_list, steps, warmup, reps=7):
         device-side wait (q4_probe_wait) long enough for the host to queue the whole region first;
         after queueing, the start event must still be pending, which proves no launch of the region
         waited for the host (else the repetition is re-queued with a longer wait);
-      * larger `steps`: the region is one replay of a HIP graph of the `steps` launches (its ~10 us
+      * larger `steps`, and any run under rocprofv3: the region is one replay of a HIP graph of the `steps` launches (its ~10 us
         of graph-launch cost is then under 0.5% of the region)."""
     import torch
     from q4llm._lib import LIB
@@ -97,7 +97,8 @@ def timed_steps(fn_list, steps, warmup, reps=7):
         return g
 
     rot = capture(range(n))
-    stream_mode = steps <= STREAM_TIMING_MAX_STEPS
+    # under a profiler dispatches serialize and the region cannot be queued ahead: graph replays only
+    stream_mode = steps <= STREAM_TIMING_MAX_STEPS and not under_profiler()
     ga = None if stream_mode else capture(range(steps))
     out = []
     with torch.cuda.stream(s):
@@ -498,6 +499,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true", help="leave out every CPU-baseline figure")
     ap.add_argument("--skip-gemm", action="store_true")
     ap.add_argument("--skip-attn", action="store_true")
+    ap.add_argument("--skip-gemv", action="store_true",
+                    help="leave out the GEMV and probe legs (profiling the other legs; the line then has no value)")
     ap.add_argument("--skip-native", action="store_true",
                     help="skip the native-runner e2e leg (also skipped by itself under rocprofv3)")
     ap.add_argument("--sweep-gemv", action="store_true", help="time every GEMV tile config (tuning)")
@@ -523,6 +526,18 @@ def main():
 
     shapes = [(5120, 3072), (16384, 3072), (3072, 8192)]
     results = {}
+    if a.skip_gemv:
+        out = {"metric": "int4 GEMV achieved HBM GB/s (% of peak) + batch-1 decode tokens/s, 3B-shape", "value": None,
+               "unit": "GB/s", "note": "--skip-gemv: profiling run of the other legs"}
+        if not a.skip_gemm:
+            out["gemm_f16"] = bench_gemm(dev, GEMM_SHAPES if a.gemm_shapes is None else
+                                         [tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes])
+        if not a.skip_attn:
+            out["attn_decode"] = bench_attn(dev)
+        if not a.skip_e2e:
+            out["e2e_3b"] = bench_e2e(dev, native=not a.skip_native, cpu=not a.skip_cpu)[0]
+        print(json.dumps(out), flush=True)
+        return 0
     for (N, K) in shapes:
         gb = GemvBench(dev, N, K)
         rel = gb.check()

@@ -453,6 +453,7 @@ int main(int argc, char** argv) {
   const int64_t qkv_n = static_cast<int64_t>(m.n_heads + 2 * m.n_kv) * m.head_dim;
   for (auto& ly : r.layers) {
     ly.wqkv_t = t16(ly.wqkv_q, ly.wqkv_s, qkv_n, m.dim, Q4_PAIR_ROPE);
+    ly.wo_t = t16(ly.wo_q, ly.wo_s, m.dim, static_cast<int64_t>(m.n_heads) * m.head_dim, Q4_PAIR_NONE);
     ly.wgu_t = t16(ly.wgu_q, ly.wgu_s, 2LL * m.inter, m.dim, Q4_PAIR_SWIGLU);
     ly.wdown_t = t16(ly.wdown_q, ly.wdown_s, m.dim, m.inter, Q4_PAIR_NONE);
   }

@@ -642,11 +642,13 @@ bool mx_fits(const MxCfg& c, int n_tiles, int nblk) {
 }
 
 // Fixed rule. Measured entries for the Llama-3.2-3B decode shapes (graph replays over rotating
-// weights on one MI355X; VALU kernel in brackets): qkv 5120x3072 + RoPE pairs 5.31 us [5.62],
-// gate/up 16384x3072 + SwiGLU pairs 7.74 us [8.81], down 3072x8192 6.03 us [6.54], LM head
-// 128256x3072 36.6 us [55.6]; the 3072x3072 o-projection stays on the VALU kernel (3.87 us vs
-// 4.03). Other shapes: the first fitting entry in list order (8 used rows per block when 16 give
-// fewer than 256 row blocks), grid-stride entries for matrices taller than 4096 row blocks.
+// weights on one MI355X; VALU kernel in brackets), reference layout: qkv 5120x3072 + RoPE pairs
+// 5.31 us [5.62], gate/up 16384x3072 + SwiGLU pairs 7.74 us [8.81], down 3072x8192 6.03 us [6.54],
+// LM head 128256x3072 36.6 us [55.6]; the 3072x3072 o-projection stays on the VALU kernel there.
+// T16 layout (nontemporal weight loads): qkv 5.02, gate/up 7.48, down 5.26, LM head 36.2 and the
+// o-projection 3.09 us on entry 4. Other shapes: the first fitting entry in list order (8 used rows
+// per block when 16 give fewer than 256 row blocks), grid-stride entries for matrices taller than
+// 4096 row blocks.
 // Returns -1 when the VALU kernel should run.
 int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair, bool tiled) {
   auto fits = [&](int i) { return mx_fits(kMxCfgs[i], n_tiles, nblk) && (!pair || kMxCfgs[i].rpb == 16); };
@@ -657,7 +659,9 @@ int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair, bool tiled) {
   }
   if (n_tiles == 6 && pair) return n_rb16 <= 512 ? 11 : 8;
   if (n_tiles == 6 && !pair && n_rb16 > 4096) return 19;
-  if (n_tiles == 6 && !pair && n_rb16 == 192 && !tiled) return -1;
+  // the 3072x3072 o-projection: the VALU kernel on the reference layout (3.25 us) beats the matrix
+  // cores there, while on the T16 layout full 16-row blocks, 3 waves of 2 tiles, take 3.09 us
+  if (n_tiles == 6 && !pair && n_rb16 == 192) return tiled ? 4 : -1;
   if (n_tiles == 16 && !pair && n_rb16 <= 512) return 13;
   if (!pair && n_rb16 > 4096) {
     for (int i = 0; i < kNumMxCfgs; ++i)

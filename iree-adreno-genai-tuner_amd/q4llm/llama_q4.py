@@ -183,9 +183,8 @@ class _ModelC(C.Structure):
                [("embed_t", _T16C)]
 
 
-# Decode projections that get a T16 copy, with the pairing their GEMV epilogue needs. The o-projection
-# keeps the reference layout: its VALU GEMV is as fast as the matrix-core one on T16 at 3072x3072.
-_T16_ROLES = {"wqkv": ops.PAIR_ROPE, "wgu": ops.PAIR_SWIGLU, "wdown": ops.PAIR_NONE}
+# Decode projections that get a T16 copy, with the pairing their GEMV epilogue needs.
+_T16_ROLES = {"wqkv": ops.PAIR_ROPE, "wo": ops.PAIR_NONE, "wgu": ops.PAIR_SWIGLU, "wdown": ops.PAIR_NONE}
 
 
 class LlamaQ4(nn.Module):
