@@ -296,6 +296,14 @@ int q4llm_step_noalloc(const q4llm_model* m, const int32_t* tokens, int C, const
                        const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
                        void* stream);
 
+/* q4llm_step, then start[0] += C on the device, done by the step's last kernel: the decode loop's
+ * position step (pos += 1, runner/llm_runner.c:233-245) without a kernel of its own. With
+ * tokens == next, a graph of one q4llm_step_feed call replays consecutive decode steps with no
+ * host input between them. */
+int q4llm_step_feed(const q4llm_model* m, const int32_t* tokens, int C, int32_t* start,
+                    const int32_t* last, void* const* caches, int L, int32_t* next, float* logits,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* start[0] += delta on the device, stream ordered: the decode loop's position step (pos += 1,
  * runner/llm_runner.c:233-245) for a loop that feeds the next token and position back on the
  * device; one kernel, so it can be captured with q4llm_step into one graph. */

@@ -281,12 +281,30 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
   if (threadIdx.x == 0) ws[blockIdx.x] = r;
 }
 
-__global__ __launch_bounds__(256) void argmax_final_kernel(const Best* __restrict__ ws, int n, int32_t* __restrict__ out) {
+// advance: null, or the decode position, advanced by delta once the token is written (a decode
+// graph that feeds itself needs no kernel of its own for it).
+__global__ __launch_bounds__(256) void argmax_final_kernel(const Best* __restrict__ ws, int n, int32_t* __restrict__ out,
+                                                           int32_t* __restrict__ advance, int delta) {
+  // every partial a thread reads in one pass is loaded before any is compared (one memory round
+  // trip per 2048 partials)
+  constexpr int kPer = 8;
   Best b{-INFINITY, INT32_MAX};
-  for (int i = threadIdx.x; i < n; i += 256)
-    if (better(ws[i].v, ws[i].i, b.v, b.i)) b = ws[i];
+  for (int base = 0; base < n; base += 256 * kPer) {
+    Best v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = base + u * 256 + threadIdx.x;
+      v[u] = i < n ? ws[i] : Best{-INFINITY, INT32_MAX};
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if (better(v[u].v, v[u].i, b.v, b.i)) b = v[u];
+  }
   const Best r = block_best(b);
-  if (threadIdx.x == 0) out[0] = r.i;
+  if (threadIdx.x == 0) {
+    out[0] = r.i;
+    if (advance) advance[0] += delta;
+  }
 }
 
 int argmax_blocks(int64_t V) {
@@ -375,9 +393,22 @@ extern "C" int argmax_f32(const float* logits, int64_t V, int32_t* out, void* wo
   const int nb = argmax_blocks(V);
   const hipStream_t st = as_stream(stream);
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(nb), dim3(256), 0, st, logits, V, static_cast<Best*>(workspace));
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, static_cast<const Best*>(workspace), nb, out);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, static_cast<const Best*>(workspace), nb, out,
+                     nullptr, 0);
   return launch_status();
 }
+
+namespace q4 {
+static_assert(sizeof(ArgBest) == sizeof(Best) && alignof(ArgBest) == alignof(Best), "one partial layout");
+
+int argmax_final_launch(const ArgBest* partials, int n, int32_t* out, int32_t* advance, int delta, hipStream_t st) {
+  if (!partials || !out) return Q4_ERR_NULL;
+  if (n <= 0) return Q4_ERR_SHAPE;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, reinterpret_cast<const Best*>(partials), n, out,
+                     advance, delta);
+  return launch_status();
+}
+}  // namespace q4
 
 namespace q4 {
 namespace {

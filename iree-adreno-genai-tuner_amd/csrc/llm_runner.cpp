@@ -256,8 +256,8 @@ void* need(Packed& pk, const std::string& name) {
 // ------------------------------------------------------------------------------------------------
 
 // Decode entry points (C == 1) feed themselves: their token buffer is their `next` buffer (q4llm_step
-// reads the tokens in its first kernel and writes next in its last) and the graph ends by adding 1
-// to start (q4llm_advance_position), so after a call the device inputs already hold what the
+// reads the tokens in its first kernel and writes next in its last) and the step is q4llm_step_feed,
+// whose last kernel adds 1 to start, so after a call the device inputs already hold what the
 // following decode call passes; `call` then skips the host-to-device copy.
 struct EntryPoint {
   int C = 0, L = 0;
@@ -279,9 +279,14 @@ struct Runner {
   int host_cap = 0;
   std::map<std::pair<int, int>, EntryPoint> eps;
 
-  void raw_step(EntryPoint& e) {
-    Q4_OK_OR_DIE(q4llm_step(&model, e.tokens, e.C, e.start, e.last, caches.data(), e.L, e.next, nullptr, e.ws,
-                            e.ws_bytes, stream));
+  // decode entry points (feed) advance their own start in the step's last kernel
+  void raw_step(EntryPoint& e, bool feed = false) {
+    if (feed)
+      Q4_OK_OR_DIE(q4llm_step_feed(&model, e.tokens, e.C, e.start, e.last, caches.data(), e.L, e.next, nullptr, e.ws,
+                                   e.ws_bytes, stream));
+    else
+      Q4_OK_OR_DIE(q4llm_step(&model, e.tokens, e.C, e.start, e.last, caches.data(), e.L, e.next, nullptr, e.ws,
+                              e.ws_bytes, stream));
   }
 
   EntryPoint& entry(int C, int L) {
@@ -311,8 +316,7 @@ struct Runner {
     HIP_OK(hipMemset(e.io, 0, sizeof(int32_t) * (C + 3)));
     hipGraph_t g = nullptr;
     HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-    raw_step(e);
-    if (C == 1) Q4_OK_OR_DIE(q4llm_advance_position(e.start, 1, stream));
+    raw_step(e, C == 1);
     HIP_OK(hipStreamEndCapture(stream, &g));
     HIP_OK(hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0));
     HIP_OK(hipGraphDestroy(g));

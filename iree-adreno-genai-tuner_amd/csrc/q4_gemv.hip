@@ -29,6 +29,7 @@
 //               sum of x. Four dot2 and five bit operations per 8 nibbles.
 //     Both paths accumulate in fp32.
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <array>
 #include <cstdlib>
@@ -253,14 +254,7 @@ __device__ __forceinline__ uint4 swiglu4(const uint4& gv, const uint4& uv) {
 // ------------------------------------------------------------------------------------------
 constexpr int kEpiNone = 0, kEpiSwiglu = 1, kEpiRope = 2;
 
-struct EpiArgs {
-  const float* cos_t;
-  const float* sin_t;
-  uint16_t* kc;
-  uint16_t* vc;
-  const int32_t* start;
-  int n_q, n_kv, hd, max_ctx;
-};
+using EpiArgs = GemvEpi;
 
 __device__ __forceinline__ void rope_pair(float x1, float x2, float c1, float s1, float c2, float s2, float& lo,
                                           float& hi) {
@@ -706,9 +700,7 @@ int set_lds_limit(KernelFn fn, size_t bytes) {
 
 // Matrix-core GEMV for fp32 x / fp32 y (q4_gemv_mx.hip); Q4_ERR_UNSUPPORTED for shapes it does not
 // take. `ep` points at an EpiArgs (same field order as the kernel's own struct).
-int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
-                   const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
-                   const void* ep, hipStream_t stream, bool tiled);
+
 
 // Runs config `cfg` (-1 = automatic choice) with `grid_override` workgroups (0 = automatic).
 // Automatic fp32-x / fp32-y launches go to the matrix-core kernel when it takes the shape.

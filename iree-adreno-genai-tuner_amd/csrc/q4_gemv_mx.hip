@@ -39,6 +39,7 @@
 // Global reads are raw buffer loads: rows past N, k past K and groups past K/G read out of range
 // and return zeros without memory traffic, so the load stream has no branches.
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <array>
 #include <cstdlib>
@@ -78,14 +79,14 @@ __device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 constexpr int kProNone = 0, kProNorm = 1;
 constexpr int kEpiNone = 0, kEpiSwiglu = 1, kEpiRope = 2;
 
-struct MxEpi {
-  const float* cos_t;
-  const float* sin_t;
-  uint16_t* kc;
-  uint16_t* vc;
-  const int32_t* start;
-  int n_q, n_kv, hd, max_ctx;
-};
+using MxEpi = GemvEpi;
+
+// argmax order of llama_ops.hip: the first index of the maximum, NaN above every number
+__device__ __forceinline__ bool arg_better(float a, int32_t ia, float b, int32_t ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
 #pragma clang fp contract(off)
@@ -326,6 +327,7 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
 
   Regs R0;
   const int wg0 = blockIdx.x;
+  ArgBest best{-INFINITY, INT32_MAX};  // argmax of the rows this thread stores (plain epilogue)
 
   // ---- prologue: x (optionally x * norm weight) -> per-group integer limbs in LDS ----
   // Single pass: thread tid owns 16-k block tid (the host guarantees 64 W >= blocks); the G/16
@@ -502,7 +504,9 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
       const int row = rb * RPB + v;
       if (v < RPB && row < N) {
         const float r = row_total(v);
-        y[row] = residual ? residual[row] + r : r;
+        const float out = residual ? residual[row] + r : r;
+        y[row] = out;
+        if (arg_better(out, row, best.v, best.i)) best = ArgBest{out, row};
       }
     } else if constexpr (EPI == kEpiSwiglu) {
       const int p = rb * 8 + v;
@@ -558,6 +562,18 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
       issue((wg0 + (it + 2) * stride) * RBW + rbl, R0);
       if (it + 1 < my) compute(wg0 + (it + 1) * stride, R1, 1);
       issue((wg0 + (it + 3) * stride) * RBW + rbl, R1);
+    }
+  }
+  if constexpr (EPI == kEpiNone) {
+    // per-workgroup argmax partial of the stored rows (they all sit in the first wave: 16 RBW <= 64)
+    if (ea.amax && wave == 0) {
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(best.v, m, 64);
+        const int32_t oi = __shfl_xor(best.i, m, 64);
+        if (arg_better(ov, oi, best.v, best.i)) best = ArgBest{ov, oi};
+      }
+      if (lane == 0) ea.amax[blockIdx.x] = best;
     }
   }
 }
@@ -706,7 +722,7 @@ bool gemv_mx_takes_t16(int64_t N, int64_t K, int group, bool pair) {
 // epilogue 0 = none, 1 = SwiGLU pairs, 2 = RoPE + KV pairs (ep describes the latter).
 int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
                    const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
-                   const void* ep, hipStream_t stream, bool tiled) {
+                   const GemvEpi* ep, hipStream_t stream, bool tiled, int* grid_out) {
   if (!tiled && getenv("Q4_GEMV_NO_MX")) return Q4_ERR_UNSUPPORTED;
   if (K % 32 || K > 16384 || N <= 0) return Q4_ERR_UNSUPPORTED;
   if (group != 32 && group != 128) return Q4_ERR_UNSUPPORTED;
@@ -715,8 +731,10 @@ int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* 
   if (!aligned(qweight, 16) || !aligned(x, 16) || (aux && !aligned(aux, 16))) return Q4_ERR_UNSUPPORTED;
   if (epilogue != kEpiNone && (N % 2 || residual)) return Q4_ERR_UNSUPPORTED;
   MxEpi ea{};
+  if (ep) ea.amax = epilogue == kEpiNone ? ep->amax : nullptr;
   if (epilogue == kEpiRope) {
-    ea = *static_cast<const MxEpi*>(ep);
+    ea = *ep;
+    ea.amax = nullptr;
     // 8 consecutive pairs stay inside one head; head_dim / 2 a power of two (shift-based row map)
     if (ea.hd <= 0 || (ea.hd / 2) % 8 || ((ea.hd / 2) & (ea.hd / 2 - 1))) return Q4_ERR_UNSUPPORTED;
   }
@@ -747,6 +765,8 @@ int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* 
     const int64_t cap = gv && atoi(gv) > 0 ? atoi(gv) : 1024;
     grid = n_wg < cap ? n_wg : cap;
   }
+  if (ea.amax && grid > ep->amax_cap) return Q4_ERR_WORKSPACE;
+  if (grid_out) *grid_out = static_cast<int>(grid);
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(64 * W), lds, stream, qweight, scales, x, aux, eps, y,
                      residual, static_cast<int>(N), static_cast<int>(K), n_tiles, static_cast<int>(n_rb), ea);
   return launch_status();

@@ -8,7 +8,47 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "q4llm.h"
+
 namespace q4 {
+
+// (value, index) of a running argmax: the first index of the maximum, a NaN counting as larger than
+// every number (torch.argmax, llama_q4.py:239).
+struct ArgBest {
+  float v;
+  int32_t i;
+};
+
+// Arguments of the decode GEMVs' fused epilogues: the RoPE tables, KV caches and position of the
+// RoPE + KV-write epilogue, and, for plain rows, an optional buffer of per-workgroup argmax partials
+// of the stored rows (one ArgBest per workgroup of the launch; null: none).
+struct GemvEpi {
+  const float* cos_t;
+  const float* sin_t;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int32_t* start;
+  int n_q, n_kv, hd, max_ctx;
+  ArgBest* amax;
+  int amax_cap;  // entries amax holds: a launch needing more workgroups is refused
+};
+
+// Matrix-core decode GEMV (q4_gemv_mx.hip); `tiled`: the weights are a T16 copy. Returns
+// Q4_ERR_UNSUPPORTED (nothing launched) for shapes it does not take; *grid_out (if not null) receives
+// the number of workgroups launched.
+int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
+                   const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
+                   const GemvEpi* ep, hipStream_t stream, bool tiled, int* grid_out = nullptr);
+
+// q4_gemv_t16 with argmax partials of the stored rows written to amax (amax_cap entries; plain rows
+// only); *grid receives the number of partials written.
+int gemv_t16_launch(const void* tiles, const void* tile_scales, const float* x, int prologue, const float* aux, float eps,
+                    int epilogue, const q4_rope_kv* rope, float* y, const float* residual, int64_t N, int64_t K, int group,
+                    hipStream_t stream, ArgBest* amax, int amax_cap, int* grid);
+
+// The final pass of argmax_f32 over n partials: out[0] = the best index; with `advance` not null,
+// advance[0] += delta afterwards in the same kernel.
+int argmax_final_launch(const ArgBest* partials, int n, int32_t* out, int32_t* advance, int delta, hipStream_t st);
 
 // q4_linear_ws's GEMM on given planes (power-of-two group).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,

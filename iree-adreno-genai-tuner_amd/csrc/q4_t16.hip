@@ -13,12 +13,10 @@
 // (SwiGLU: rows p and p + N/2; RoPE: rows (head, d) and (head, d + hd/2)). Padding (rows past N,
 // k past K) is zero. Packing is a pure permutation done once, at load time, on the device.
 #include "q4_common.h"
+#include "q4_internal.h"
 
 namespace q4 {
 
-int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
-                   const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
-                   const void* ep, hipStream_t stream, bool tiled);
 bool gemv_mx_takes_t16(int64_t N, int64_t K, int group, bool pair);
 
 namespace {
@@ -116,6 +114,13 @@ extern "C" int q4_t16_pack(const int32_t* qweight, const uint16_t* scales, int64
 extern "C" int q4_gemv_t16(const void* tiles, const void* tile_scales, const float* x, int prologue, const float* aux,
                            float eps, int epilogue, const q4_rope_kv* rope, float* y, const float* residual, int64_t N,
                            int64_t K, int group, void* stream) {
+  return q4::gemv_t16_launch(tiles, tile_scales, x, prologue, aux, eps, epilogue, rope, y, residual, N, K, group,
+                             q4::as_stream(stream), nullptr, 0, nullptr);
+}
+
+int q4::gemv_t16_launch(const void* tiles, const void* tile_scales, const float* x, int prologue, const float* aux,
+                        float eps, int epilogue, const q4_rope_kv* rope, float* y, const float* residual, int64_t N,
+                        int64_t K, int group, hipStream_t stream, ArgBest* amax, int amax_cap, int* grid) {
   if (!tiles || !tile_scales || !x || !y) return Q4_ERR_NULL;
   if (prologue != Q4_PRO_NONE && prologue != Q4_PRO_RMSNORM) return Q4_ERR_DTYPE;
   if (epilogue != 0 && epilogue != Q4_EPI_SWIGLU && epilogue != Q4_EPI_ROPE_KV) return Q4_ERR_DTYPE;
@@ -131,21 +136,17 @@ extern "C" int q4_gemv_t16(const void* tiles, const void* tile_scales, const flo
     return Q4_ERR_ALIGN;
   // other workgroups may still be staging x while y is written, so x must not alias y
   if (static_cast<const void*>(x) == static_cast<const void*>(y)) return Q4_ERR_SHAPE;
-  struct {
-    const float* cos_t;
-    const float* sin_t;
-    uint16_t* kc;
-    uint16_t* vc;
-    const int32_t* start;
-    int n_q, n_kv, hd, max_ctx;
-  } ea{};
+  GemvEpi ea{};
+  if (amax && epilogue != 0) return Q4_ERR_SHAPE;  // argmax partials are for plain rows
+  ea.amax = amax;
+  ea.amax_cap = amax_cap;
   if (epilogue == Q4_EPI_ROPE_KV) {
     if (!rope->cos_t || !rope->sin_t || !rope->k_cache || !rope->v_cache || !rope->start) return Q4_ERR_NULL;
     if (rope->n_q <= 0 || rope->n_kv <= 0 || rope->max_ctx <= 0) return Q4_ERR_SHAPE;
     if (N != static_cast<int64_t>(rope->n_q + 2 * rope->n_kv) * rope->head_dim) return Q4_ERR_SHAPE;
-    ea = {rope->cos_t, rope->sin_t, rope->k_cache, rope->v_cache, rope->start, rope->n_q, rope->n_kv, rope->head_dim,
-          rope->max_ctx};
+    ea = GemvEpi{rope->cos_t, rope->sin_t, rope->k_cache, rope->v_cache, rope->start, rope->n_q, rope->n_kv,
+                 rope->head_dim, rope->max_ctx, nullptr, 0};
   }
   return gemv_mx_launch(static_cast<const int32_t*>(tiles), static_cast<const uint16_t*>(tile_scales), x, aux, eps, y,
-                        residual, N, K, group, prologue, epilogue, &ea, as_stream(stream), true);
+                        residual, N, K, group, prologue, epilogue, &ea, stream, true, grid);
 }

@@ -46,6 +46,9 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   size_t attn = 0, amax = 0;
   if (int st = attn_workspace_bytes(C, m->n_heads, m->n_kv, m->head_dim, L, &attn)) return st;
   if (int st = argmax_workspace_bytes(m->vocab, &amax)) return st;
+  // the LM head GEMV's per-workgroup argmax partials: at most one per 8 vocabulary rows (its launch
+  // entries use 8 or 16 rows per workgroup)
+  amax = std::max(amax, static_cast<size_t>((m->vocab + 7) / 8) * sizeof(q4::ArgBest));
   size_t off = 0;
   auto take = [&](size_t bytes) { const size_t o = off; off += up256(bytes); return o; };
   lo->h = take(f * C * m->dim);
@@ -125,9 +128,12 @@ extern "C" int q4llm_step_workspace_bytes(const q4llm_model* m, int C, int L, si
   return Q4_OK;
 }
 
-extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start, const int32_t* last,
-                          void* const* caches, int L, int32_t* next, float* logits, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+namespace {
+// One step; with `advance` not null, start[0] += C on the device after the next token is written
+// (q4llm_step_feed).
+int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start, const int32_t* last,
+              void* const* caches, int L, int32_t* next, float* logits, void* workspace, size_t workspace_bytes,
+              void* stream, int32_t* advance) {
   if (int st = check_model(m)) return st;
   if (!tokens || !start || !last || !caches || !next || !workspace) return Q4_ERR_NULL;
   if (C <= 0 || L <= 0 || L > m->max_ctx || C > m->max_ctx) return Q4_ERR_RANGE;
@@ -243,20 +249,42 @@ extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, co
       Q4_TRY(proj(C, act, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, lin_ws, lo.lin_bytes, stream));
     }
   }
+  if (fused && has(m->embed_t)) {
+    // one row: the final norm is the LM head's prologue, and its workgroups leave argmax partials of
+    // the logits they store, so one more kernel picks the token (and advances the position)
+    auto* partials = static_cast<q4::ArgBest*>(amax_ws);
+    int n_partials = 0;
+    Q4_TRY(q4::gemv_t16_launch(m->embed_t.tiles, m->embed_t.scales, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, 0, nullptr, lg,
+                               nullptr, m->vocab, D, m->group, st, partials,
+                               static_cast<int>(lo.amax_bytes / sizeof(q4::ArgBest)), &n_partials));
+    Q4_TRY(q4::argmax_final_launch(partials, n_partials, next, advance, C, st));
+    return Q4_OK;
+  }
   if (fused) {  // one row: the final norm is the LM head's prologue
-    if (has(m->embed_t))
-      Q4_TRY(q4_gemv_t16(m->embed_t.tiles, m->embed_t.scales, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, 0, nullptr, lg,
-                         nullptr, m->vocab, D, m->group, stream));
-    else
-      Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
-                           m->group, stream));
+    Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
+                         m->group, stream));
   } else {
     Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
     Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
   }
   Q4_TRY(argmax_f32(lg, m->vocab, next, amax_ws, lo.amax_bytes, stream));
+  if (advance) Q4_TRY(q4llm_advance_position(advance, C, stream));
 #undef Q4_TRY
   return Q4_OK;
+}
+}  // namespace
+
+extern "C" int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t* start, const int32_t* last,
+                          void* const* caches, int L, int32_t* next, float* logits, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  return step_impl(m, tokens, C, start, last, caches, L, next, logits, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int q4llm_step_feed(const q4llm_model* m, const int32_t* tokens, int C, int32_t* start, const int32_t* last,
+                               void* const* caches, int L, int32_t* next, float* logits, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!start) return Q4_ERR_NULL;
+  return step_impl(m, tokens, C, start, last, caches, L, next, logits, workspace, workspace_bytes, stream, start);
 }
 
 // ------------------------------------------------------------------------------------------------

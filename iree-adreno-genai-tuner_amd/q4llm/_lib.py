@@ -61,6 +61,7 @@ SIGNATURES = {
     "q4llm_step_workspace_bytes": [p, i32, i32, C.POINTER(sz)],
     "q4llm_step": [p, p, i32, p, p, p, i32, p, p, p, sz, p],
     "q4llm_advance_position": [p, i32, p],
+    "q4llm_step_feed": [p, p, i32, p, p, p, i32, p, p, p, sz, p],
     "q4llm_step_noalloc": [p, p, i32, p, p, p, i32, p, p, p],
     "q4_probe_read": [p, i64, p, i32, p],
     "q4_probe_empty": [i32, i32, p],

@@ -342,10 +342,12 @@ class LlamaQ4(nn.Module):
                 raise ValueError("caches must be contiguous fp16 device tensors [max_ctx, n_kv, head_dim]")
         return (C.c_void_p * len(caches))(*[c.data_ptr() for c in caches])
 
-    def _raw_step(self, tokens_d, Cn, start_d, last_d, cache_arr, L, next_d, logits_d):
+    def _raw_step(self, tokens_d, Cn, start_d, last_d, cache_arr, L, next_d, logits_d, feed=False):
+        """One q4llm_step; feed=True: q4llm_step_feed (start += C on the device after the step)."""
         ws = self.workspace(Cn, L)
-        LIB.call("q4llm_step", C.byref(self.descriptor()), ptr(tokens_d), Cn, ptr(start_d), ptr(last_d), cache_arr, L,
-                 ptr(next_d), ptr(logits_d), ptr(ws), ws.numel(), stream_of(self.device))
+        LIB.call("q4llm_step_feed" if feed else "q4llm_step", C.byref(self.descriptor()), ptr(tokens_d), Cn,
+                 ptr(start_d), ptr(last_d), cache_arr, L, ptr(next_d), ptr(logits_d), ptr(ws), ws.numel(),
+                 stream_of(self.device))
 
     # ---------------------------------------------------------------- reference API
 
@@ -382,8 +384,8 @@ class _StepGraph:
     """One (C, L) step captured into a HIP graph; inputs are copied into static device buffers.
 
     Decode graphs (C == 1) feed themselves: the token buffer is the `next` buffer (q4llm_step reads
-    the tokens in its first kernel and writes next in its last), and the graph ends by adding 1 to
-    `start`. After a replay the device inputs therefore already hold (start + 1, next token), which
+    the tokens in its first kernel and writes next in its last), and the step is q4llm_step_feed,
+    whose last kernel adds 1 to `start`. After a replay the device inputs therefore already hold (start + 1, next token), which
     is what the runner's following decode call passes, so the runner only writes them after a
     bucket switch (`feeds_back`)."""
 
@@ -414,9 +416,8 @@ class _StepGraph:
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=s):
-            model._raw_step(self.tokens, Cn, self.start, self.last, self.cache_arr, L, self.next, self.logits)
-            if self.feeds_back:
-                LIB.call("q4llm_advance_position", ptr(self.start), 1, stream_of(dev))
+            model._raw_step(self.tokens, Cn, self.start, self.last, self.cache_arr, L, self.next, self.logits,
+                            feed=self.feeds_back)
 
     def set_inputs(self, tokens, start, last):
         self.tokens.copy_(torch.as_tensor(tokens, dtype=torch.int32).reshape(-1), non_blocking=False)

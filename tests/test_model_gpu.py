@@ -173,3 +173,30 @@ def test_no_warmup_entry_points_built_mid_generation(dev):
     res = llm_runner.run(model, prompt, 20, 8, [16, 32, 64], warmup=0)
     assert sorted({L for L, _ in res["steps"]}) == [32, 64]
     assert res["tokens"] == want
+
+
+def test_step_feed_advances_position_and_matches_step(dev):
+    """q4llm_step_feed (include/q4llm.h): the same next token and logits as q4llm_step, and start
+    advanced by C on the device by the step's last kernel; tokens == next for a decode step."""
+    import ctypes as C
+    from q4llm._lib import LIB, ptr, stream_of
+    model, _ = build_pair(synth.TINY, 32, 128)
+    desc = C.byref(model.descriptor())
+    for Cn, pos in ((1, 5), (8, 16)):
+        c_a, c_b = model.new_caches(), model.new_caches()
+        toks = torch.tensor(synth.prompt_ids(Cn, 1024, seed=pos), dtype=torch.int32, device=dev)
+        last = torch.tensor([Cn - 1], dtype=torch.int32, device=dev)
+        outs = []
+        for feed, caches in ((False, c_a), (True, c_b)):
+            start = torch.tensor([pos], dtype=torch.int32, device=dev)
+            nxt = torch.empty(1, dtype=torch.int32, device=dev)
+            lg = torch.empty(model.embed.vocab, dtype=torch.float32, device=dev)
+            ws = model.workspace(Cn, 64)
+            LIB.call("q4llm_step_feed" if feed else "q4llm_step", desc, ptr(toks), Cn, ptr(start), ptr(last),
+                     model._cache_ptrs(caches), 64, ptr(nxt), ptr(lg), ptr(ws), ws.numel(), stream_of(dev))
+            torch.cuda.synchronize()
+            outs.append((int(nxt.item()), lg.clone(), int(start.item())))
+        assert outs[0][0] == outs[1][0] and torch.equal(outs[0][1], outs[1][1])
+        assert outs[0][2] == pos and outs[1][2] == pos + Cn
+        for a, b in zip(c_a, c_b):
+            assert torch.equal(a, b)
