@@ -228,8 +228,10 @@ __device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, u
 // block, splitting its tiles along K (at most TPW tiles per wave), so the workgroup has
 // W = RBW * WPB waves and converts x once for all of them. MULTI: grid-stride over groups of RBW
 // row blocks with the next group's loads in flight. RPB: used rows per 16-row block (16, or 8 to
-// spread a short matrix over more workgroups).
-template <int G, int RBW, int WPB, int TPW, bool MULTI, int PRO, int EPI, int RPB, bool TL = false>
+// spread a short matrix over more workgroups). DNP / DP: s_sleep before the first weight loads of the
+// waves without / with x blocks (below).
+template <int G, int RBW, int WPB, int TPW, bool MULTI, int PRO, int EPI, int RPB, bool TL = false, int DNP = 0,
+          int DP = 0>
 __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
     const int32_t* __restrict__ qw, const uint16_t* __restrict__ scales, const float* __restrict__ x,
     const float* __restrict__ aux, float eps, float* y, const float* residual, int N, int K, int n_tiles,
@@ -336,6 +338,14 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
   // in issue order, so x issued after the weights would make the prologue wait for the whole
   // weight stream (and a branch between the x loads and their use lets the compiler sink them
   // below the weight loads).
+  // Every workgroup reads the same x, which the previous kernel left in memory, not in this XCD's L2;
+  // issued together with the weight stream of the whole chip, its misses queue behind weight misses
+  // and the prologue, with every MFMA after it, ends late. A short s_sleep (DNP, DP: units of 64
+  // clocks) before the first weight loads lets the x misses reach the memory queues first: measured
+  // on the MI355X with the 3B decode shapes (T16 weights, rotated past the MALL), 6 on the
+  // weight-only waves takes 0.29 us off the qkv entry's 4.72 us, 6 there and 4 on the x waves 0.38 us
+  // off the gate/up entry's 7.05 us, 2 on the x waves of the 8192-wide down projection (all of its
+  // waves hold x blocks) 0.15 us off 4.87 us; the o-projection's entry gains nothing.
   const __amdgpu_buffer_rsrc_t xres = rsrc(x, static_cast<uint32_t>(K) * 4u);
   const __amdgpu_buffer_rsrc_t ares = rsrc(aux, PRO == kProNorm ? static_cast<uint32_t>(K) * 4u : 0u);
   const int beta = tid;
@@ -344,6 +354,7 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
   float ssq = 0.0f;
   constexpr int kLanesPerGroup = G / 16;
   if (!pro_wave) {
+    if constexpr (DNP > 0) __builtin_amdgcn_s_sleep(DNP);
     issue(wg0 * RBW + rbl, R0);
   } else {
     i32x4 xr[4], ar[4];
@@ -352,6 +363,10 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
       const uint32_t off = valid && 16 * beta < K ? static_cast<uint32_t>(16 * beta + 4 * i) * 4u : kOOB;
       xr[i] = load16(xres, off);
       if constexpr (PRO == kProNorm) ar[i] = load16(ares, off);
+    }
+    if constexpr (DP > 0) {
+      __builtin_amdgcn_sched_barrier(0);  // the x loads stay above the sleep
+      __builtin_amdgcn_s_sleep(DP);
     }
     issue(wg0 * RBW + rbl, R0);
     __builtin_amdgcn_sched_barrier(0);  // no x arithmetic above the weight loads
@@ -582,10 +597,12 @@ using MxFn = void (*)(const int32_t*, const uint16_t*, const float*, const float
                       int, int, MxEpi);
 
 // Explicit launch-shape list (index stable: Q4_MX_CFG selects an entry): row blocks per workgroup,
-// waves per row block, largest tiles per wave, used rows per 16-row block, grid-stride.
+// waves per row block, largest tiles per wave, used rows per 16-row block, grid-stride, and the
+// s_sleep of the weight-only and of the x waves before their first weight loads.
 struct MxCfg {
   int rbw, wpb, tpw, rpb;
   bool multi;
+  int dnp = 0, dp = 0;
 };
 constexpr MxCfg kMxCfgs[] = {
     {1, 1, 2, 16, false},   // 0: 2 tiles (K = 8 G: the tiny model's 256-wide rows)
@@ -596,12 +613,12 @@ constexpr MxCfg kMxCfgs[] = {
     {1, 3, 2, 8, false},    // 5
     {2, 3, 2, 16, false},   // 6
     {2, 3, 2, 8, false},    // 7
-    {4, 3, 2, 16, false},   // 8
+    {4, 3, 2, 16, false, 6, 4},  // 8
     {1, 6, 1, 16, false},   // 9: 6 tiles, one per wave
     {1, 6, 1, 8, false},    // 10
-    {2, 6, 1, 16, false},   // 11
+    {2, 6, 1, 16, false, 6, 0},  // 11
     {2, 6, 1, 8, false},    // 12
-    {1, 8, 2, 16, false},   // 13: 16 tiles (K = 64 G: the 8192-wide down projection)
+    {1, 8, 2, 16, false, 0, 2},  // 13: 16 tiles (K = 64 G: the 8192-wide down projection)
     {1, 8, 2, 8, false},    // 14
     {2, 8, 2, 8, false},    // 15
     {1, 16, 1, 8, false},   // 16
@@ -620,7 +637,7 @@ constexpr MxFn mx_fn() {
   } else if constexpr (G == 32 && !(I == 0 || I == 1 || I == 2 || I == 3 || I == 17)) {
     return nullptr;  // the group-32 (tiny model) shapes use a short list
   } else {
-    return q4_gemv_mx_kernel<G, c.rbw, c.wpb, c.tpw, c.multi, PRO, EPI, c.rpb, TL>;
+    return q4_gemv_mx_kernel<G, c.rbw, c.wpb, c.tpw, c.multi, PRO, EPI, c.rpb, TL, c.dnp, c.dp>;
   }
 }
 
