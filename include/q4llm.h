@@ -167,10 +167,18 @@ int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t*
 /* Workspace bytes q4_linear_ws needs for M rows of K: the fp16 hi and lo planes of x (4 * M * K). */
 int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes);
 
+/* Workspace bytes with which q4_linear_ws also splits the reduction over K for this shape (a chunk of
+ * M <= 256 rows whose output tiles alone would leave compute units idle): the planes, rounded up to
+ * 256 bytes, plus n_split * M * N fp32 partials; equal to q4_linear_workspace_bytes(M, K) where no
+ * split applies. */
+int q4_linear_ws_split_bytes(int64_t M, int64_t N, int64_t K, int group, size_t* bytes);
+
 /* q4_linear (QLinear.forward at M > 1, llama_q4.py:72) with a caller workspace: x is split once into
  * fp16 hi/lo planes in `workspace`, then a multi-stage matrix-core pipeline streams both planes and
  * the packed int4 weights (two launches on `stream`). Same contract and accuracy as q4_linear;
- * workspace >= q4_linear_workspace_bytes(M, K), 16-byte aligned. */
+ * workspace >= q4_linear_workspace_bytes(M, K), 16-byte aligned. With workspace_bytes >=
+ * q4_linear_ws_split_bytes(M, N, K, group) the GEMM may split K over several workgroups per output
+ * tile and add their partials (in a fixed order) and the residual in a third launch. */
 int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
                  const float* residual, int64_t N, int64_t K, int group, void* workspace,
                  size_t workspace_bytes, void* stream);

@@ -50,9 +50,19 @@ int gemv_t16_launch(const void* tiles, const void* tile_scales, const float* x, 
 // advance[0] += delta afterwards in the same kernel.
 int argmax_final_launch(const ArgBest* partials, int n, int32_t* out, int32_t* advance, int delta, hipStream_t st);
 
-// q4_linear_ws's GEMM on given planes (power-of-two group).
+// K split of a prefill projection: n_split workgroups per output tile, nk_split 64-k stages each.
+struct LinearSplit {
+  int n_split, nk_split;
+};
+LinearSplit linear_split_plan(int64_t M, int64_t N, int64_t K, int group);
+// bytes of K-split partials q4_linear_planes uses for this shape (0: it takes no K split)
+size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group);
+
+// q4_linear_ws's GEMM on given planes (power-of-two group); with `part` (at least
+// linear_split_part_bytes, 16-byte aligned) it may split K and reduce the partials in a second kernel.
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
-                     float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st);
+                     float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st,
+                     float* part = nullptr, size_t part_bytes = 0);
 // The gate/up projection with silu(gate) * up written as the [M, N / 2] planes oh / ol (ol = oh + M N / 2)
 // of the down projection; Q4_ERR_UNSUPPORTED when the shape does not take the fused tile (the caller then
 // runs q4_linear_planes + silu_mul_planes).

@@ -351,10 +351,14 @@ __device__ __forceinline__ float silu_mul_exact(float g, float u) {
 // a wave hold the gate and up values of the same 32 outputs in the same lanes; the epilogue writes
 // silu(gate) * up for [M, I] into the fp16 (hi, lo) planes at Y (hi) and Y + M I (lo), the input of the
 // down projection. R must be null.
+// Split over K (n_split > 1, EPI = 0): workgroup s * tiles + t takes output tile t over the 64-k stages
+// [s * nk_split, (s + 1) * nk_split) (whole groups) and writes its sum, without the residual, to the
+// partial buffer P[s] ([M, N] fp32 each); linear_reduce_kernel then adds the residual and the partials.
 template <int BM, int BN, int WM, int WN, int NST, int KS, int EPI = 0>
 __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
-    const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n) {
+    const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n,
+    int n_split = 1, int nk_split = 0, float* __restrict__ P = nullptr) {
   using G = LinWsCfg<BM, BN, WM, WN, NST, KS>;
   static_assert(EPI == 0 || (G::TN % 2 == 0 && G::WTN % 64 == 0 && BN % 64 == 0), "SwiGLU pairs tiles 2j, 2j + 1");
   // weight row of virtual column v
@@ -367,7 +371,9 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     }
   };
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int n_tiles = static_cast<int>(gridDim.x) / n_split;
+  const int ksp = static_cast<int>(blockIdx.x) / n_tiles, tile = static_cast<int>(blockIdx.x) - ksp * n_tiles;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
   const int gshift = __builtin_ctz(group);  // the host passes power-of-two groups only
   const int spr = K >> gshift;
@@ -414,9 +420,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
   // Every step issues the same loads (steps past K load zeros into a free stage), so the number of
   // vector-memory operations in flight is the same on every path: the exact waits below and the
   // compiler's own waits for the scale registers then agree.
+  const int nk = K / 64;
+  const int kt_begin = n_split > 1 ? ksp * nk_split : 0;
+  const int kt_end = n_split > 1 ? min(nk, kt_begin + nk_split) : nk;
   auto issue = [&](int kt, int stage) {
     const int k0 = kt * 64;
-    const bool kin = k0 < K;
+    const bool kin = kt < kt_end;
     unsigned char* sh = lds + stage * G::kStage;
     unsigned char* sl = sh + BM * G::kXRow;
     unsigned char* sw = sl + BM * G::kXRow;
@@ -469,7 +478,6 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
 
   const int arow = wm * G::WTM + (lane & 31);
   const int brow = wn * G::WTN + (lane & 31);
-  const int nk = K / 64;
   // Every load of a step (x planes, weights, scales) goes straight to LDS; when at most NST-2 steps'
   // loads of this wave are in flight, its part of step kt has landed, and the barrier publishes the
   // whole stage. No VGPR is loaded in the loop, so the compiler adds no waits of its own.
@@ -541,8 +549,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     }
   };
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) step(kt);
+  for (int s = 0; s < NST - 1; ++s) issue(kt_begin + s, (kt_begin + s) % NST);
+  for (int kt = kt_begin; kt < kt_end; ++kt) step(kt);
 
   if constexpr (KS > 1) {
     // k-split: wave groups 1..KS-1 hand their sums to group 0 through LDS (the stage memory; the
@@ -602,9 +610,31 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
         const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
         if (row < M && col < N) {
           const int64_t o = static_cast<int64_t>(row) * N + col;
-          Y[o] = R ? R[o] + acc[i][j][e] : acc[i][j][e];
+          if (n_split > 1) P[static_cast<int64_t>(ksp) * M * N + o] = acc[i][j][e];
+          else Y[o] = R ? R[o] + acc[i][j][e] : acc[i][j][e];
         }
       }
+}
+
+// y = residual + sum_s P[s] over n = M N / 4 float4 elements, the splits added in ascending order
+// (fixed, so results do not depend on scheduling); y may alias the residual.
+__global__ __launch_bounds__(256) void linear_reduce_kernel(const float4* __restrict__ P, const float4* R, float4* Y,
+                                                            int64_t n, int n_split) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  float4 a = P[i];
+  for (int s = 1; s < n_split; ++s) {
+    const float4 b = P[s * n + i];
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+  if (R) {
+    const float4 r = R[i];
+    a = make_float4(r.x + a.x, r.y + a.y, r.z + a.z, r.w + a.w);
+  }
+  Y[i] = a;
 }
 
 struct LinWsTile {
@@ -631,7 +661,7 @@ constexpr LinWsTile kLinWsTiles[] = {
     {32, 96, 1, 3, 4, 1},    // 15: 3 waves of 32x32
 };
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
-                         int, int, int, int);
+                         int, int, int, int, int, int, float*);
 template <int I>
 constexpr LinWsFn lin_ws_fn() {
   constexpr LinWsTile t = kLinWsTiles[I];
@@ -703,18 +733,64 @@ int planes_args(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t
 }
 }  // namespace
 
+// K split of the 64x256 tile (entry 12) for a chunk of M <= 256 rows whose tiles alone would leave
+// CUs idle: about 256 / tiles splits, each a whole number of groups (64-k stages, at least one group).
+LinearSplit linear_split_plan(int64_t M, int64_t N, int64_t K, int group) {
+  LinearSplit p{1, 0};
+  if (M <= 0 || M > 256 || K % 64 || group <= 0) return p;
+  const int64_t tiles = ((M + 63) / 64) * ((N + 255) / 256);
+  const int64_t s0 = 256 / tiles;
+  if (s0 < 2) return p;
+  const int nk = static_cast<int>(K / 64), gst = group > 64 ? group / 64 : 1;
+  int nk_s = static_cast<int>((nk + s0 - 1) / s0);
+  nk_s = (nk_s + gst - 1) / gst * gst;
+  const int S = (nk + nk_s - 1) / nk_s;
+  if (S < 2) return p;
+  p.n_split = S;
+  p.nk_split = nk_s;
+  return p;
+}
+
+size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group) {
+  const LinearSplit p = linear_split_plan(M, N, K, group);
+  return p.n_split > 1 ? static_cast<size_t>(p.n_split) * M * N * sizeof(float) : 0;
+}
+
 // The pipelined GEMM on x given as fp16 (hi, lo) planes (store_x_planes layout, [M, K] each);
 // power-of-two groups only. Tile rule from a sweep of every entry over the 3B prefill shapes at
-// M = 128, 256 and 1024 (graph replays on one MI355X): the 32x64 k-split tile while it gives at most
-// 768 workgroups (every M <= 256 chunk of the 3072-, 5120- and 8192-wide projections), else 64x64.
-// Q4_LINEAR_CFG overrides.
+// M = 128, 256 and 1024 (graph replays on one MI355X): with a partial buffer `part` of at least
+// linear_split_part_bytes, the K-split 64x256 tile where linear_split_plan gives a split (every M <= 256
+// chunk of the 3072-, 5120- and 8192-wide projections), then linear_reduce_kernel; otherwise the 32x64
+// k-split tile while it gives at most 768 workgroups, else 64x64. Q4_LINEAR_CFG overrides (no K split).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
-                     float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st) {
+                     float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st, float* part,
+                     size_t part_bytes) {
   if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
   if (!y) return Q4_ERR_NULL;
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
+  const LinearSplit sp = linear_split_plan(M, N, K, group);
+  if (ti < 0 && part && sp.n_split > 1 && part_bytes >= linear_split_part_bytes(M, N, K, group) &&
+      (M * N) % 4 == 0 && aligned(part, 16) && aligned(y, 16) && (!res || aligned(res, 16)) &&
+      static_cast<int64_t>(sp.n_split) * M * N < (int64_t{1} << 31)) {
+    constexpr int T = 12;
+    const LinWsTile& t = kLinWsTiles[T];
+    const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
+    const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
+    if (kLinWsLds[T] > 64 * 1024) {
+      Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kLinWsFns[T]),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[T])));
+    }
+    hipLaunchKernelGGL(kLinWsFns[T], dim3(tiles * sp.n_split), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[T], st, xh,
+                       xl, qw, sc, y, res, (int)M, (int)N, (int)K, group, tiles_n, sp.n_split, sp.nk_split, part);
+    if (int e = launch_status()) return e;
+    const int64_t n4 = M * N / 4;
+    hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(part), reinterpret_cast<const float4*>(res),
+                       reinterpret_cast<float4*>(y), n4, sp.n_split);
+    return launch_status();
+  }
   // Rule from a sweep at M = 128, 256, 1024: the 32x64 k-split tile while it gives <= 768 workgroups,
   // else 64x64; and 64x256 when, at M <= 256, it alone gives one workgroup per CU (the gate/up
   // projection of a 256-row chunk: 256x16384x3072 82 -> 69 us, x re-read over 4x fewer column tiles).
@@ -731,7 +807,7 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[ti])));
   }
   hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
-                     (int)M, (int)N, (int)K, group, tiles_n);
+                     (int)M, (int)N, (int)K, group, tiles_n, 1, 0, nullptr);
   return launch_status();
 }
 
@@ -756,12 +832,14 @@ int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, c
   const int tiles_n = static_cast<int>(N / t.bn);
   const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
   hipLaunchKernelGGL(fn, dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), lds, st, xh, xl, qw, sc,
-                     reinterpret_cast<float*>(oh), nullptr, (int)M, (int)N, (int)K, group, tiles_n);
+                     reinterpret_cast<float*>(oh), nullptr, (int)M, (int)N, (int)K, group, tiles_n, 1, 0, nullptr);
   return launch_status();
 }
 
+// ws holds the planes (M K fp16 each) and, past them (from a 256-byte boundary), ws_bytes permitting,
+// the K-split partials.
 int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint16_t* sc, float* y, const float* res,
-                        int64_t N, int64_t K, int group, void* ws, hipStream_t st) {
+                        int64_t N, int64_t K, int group, void* ws, size_t ws_bytes, hipStream_t st) {
   // the pipelined kernel indexes groups by shifts: other group sizes take the workspace-free kernel
   if (group & (group - 1)) return q4_linear_launch(x, M, qw, sc, y, res, N, K, group, -1, st);
   uint16_t* xh = static_cast<uint16_t*>(ws);
@@ -770,7 +848,9 @@ int q4_linear_ws_launch(const float* x, int64_t M, const int32_t* qw, const uint
   hipLaunchKernelGGL(split_x_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, st, x, xh, xl,
                      chunks);
   if (int e = launch_status()) return e;
-  return q4_linear_planes(xh, xl, M, qw, sc, y, res, N, K, group, st);
+  const size_t planes = (static_cast<size_t>(M) * K * 4 + 255) / 256 * 256;
+  float* part = ws_bytes > planes ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + planes) : nullptr;
+  return q4_linear_planes(xh, xl, M, qw, sc, y, res, N, K, group, st, part, part ? ws_bytes - planes : 0);
 }
 
 }  // namespace q4
@@ -802,6 +882,15 @@ extern "C" int q4_linear_workspace_bytes(int64_t M, int64_t K, size_t* bytes) {
   return Q4_OK;
 }
 
+extern "C" int q4_linear_ws_split_bytes(int64_t M, int64_t N, int64_t K, int group, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 || group <= 0) return Q4_ERR_SHAPE;
+  const size_t planes = (static_cast<size_t>(M) * K * 4 + 255) / 256 * 256;
+  const size_t part = (group & (group - 1)) == 0 ? q4::linear_split_part_bytes(M, N, K, group) : 0;
+  *bytes = part ? planes + part : static_cast<size_t>(M) * K * 4;
+  return Q4_OK;
+}
+
 extern "C" int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,
                             const float* residual, int64_t N, int64_t K, int group, void* workspace,
                             size_t workspace_bytes, void* stream) {
@@ -809,7 +898,8 @@ extern "C" int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, c
   if (!workspace) return Q4_ERR_NULL;
   if (workspace_bytes < static_cast<size_t>(M) * static_cast<size_t>(K) * 4) return Q4_ERR_WORKSPACE;
   if (!q4::aligned(workspace, 16)) return Q4_ERR_ALIGN;
-  return q4::q4_linear_ws_launch(x, M, qweight, scales, y, residual, N, K, group, workspace, q4::as_stream(stream));
+  return q4::q4_linear_ws_launch(x, M, qweight, scales, y, residual, N, K, group, workspace, workspace_bytes,
+                                 q4::as_stream(stream));
 }
 
 extern "C" int q4_linear(const float* x, int64_t M, const int32_t* qweight, const uint16_t* scales, float* y,

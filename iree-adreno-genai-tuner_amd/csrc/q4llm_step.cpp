@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstddef>
 #include <cstdlib>
@@ -30,8 +31,8 @@
 namespace {
 
 struct Layout {
-  size_t h, x, qkv, o, gu, act, xf, logits, attn, amax, lin, total;
-  size_t attn_bytes, amax_bytes, lin_bytes;
+  size_t h, x, qkv, o, gu, act, xf, logits, attn, amax, lin, part, total;
+  size_t attn_bytes, amax_bytes, lin_bytes, part_bytes;
 };
 
 size_t up256(size_t b) { return (b + 255) / 256 * 256; }
@@ -74,6 +75,17 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   }
   lo->lin = take(lin);
   lo->lin_bytes = lin;
+  // K-split partials of the prefill projections (the largest of the four)
+  size_t part = 0;
+  if (C > 1) {
+    for (const int64_t* nk : {std::array<int64_t, 2>{nq + 2 * nkv, m->dim}.data(), std::array<int64_t, 2>{m->dim, nq}.data(),
+                              std::array<int64_t, 2>{2 * static_cast<int64_t>(m->inter), m->dim}.data(),
+                              std::array<int64_t, 2>{m->dim, m->inter}.data()})
+      if (linear_fits(static_cast<int>(nk[1]), m->group) && (m->group & (m->group - 1)) == 0)
+        part = std::max(part, q4::linear_split_part_bytes(C, nk[0], nk[1], m->group));
+  }
+  lo->part = take(part);
+  lo->part_bytes = part;
   lo->total = off;
   return Q4_OK;
 }
@@ -154,6 +166,7 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   void* attn_ws = ws + lo.attn;
   void* amax_ws = ws + lo.amax;
   void* lin_ws = ws + lo.lin;
+  float* part = lo.part_bytes ? reinterpret_cast<float*>(ws + lo.part) : nullptr;
 
   const int D = m->dim, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv;
   const int nq_w = nh * hd, qkv_w = (nh + 2 * nkv) * hd;
@@ -196,7 +209,8 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
                                 qkv_w, D, m->group, stream));
     } else if (planes) {
       Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st));
-      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st, part,
+                                  lo.part_bytes));
       Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
@@ -206,7 +220,7 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
     if (planes) {
       Q4_TRY(q4::attn_bucket_planes(qkv, qkv_w, kc, vc, xh, xl, C, nh, nkv, hd, L, start, scale, attn_ws,
                                     lo.attn_bytes, st));
-      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st));
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st, part, lo.part_bytes));
     } else {
       Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
       if (has(ly.wo_t))
@@ -235,12 +249,15 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       uint16_t* al = ah + static_cast<int64_t>(C) * m->inter;
       const int fused = q4::q4_linear_planes_swiglu(xh, xl, C, ly.wgu_q, ly.wgu_s, ah, al, 2 * m->inter, D, m->group, st);
       if (fused == Q4_OK) {
-        Q4_TRY(q4::q4_linear_planes(ah, al, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
+        Q4_TRY(q4::q4_linear_planes(ah, al, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
+                                    lo.part_bytes));
       } else {
         if (fused != Q4_ERR_UNSUPPORTED) return fused;
-        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st));
+        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st, part,
+                                    lo.part_bytes));
         Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
-        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st));
+        Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
+                                    lo.part_bytes));
       }
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));

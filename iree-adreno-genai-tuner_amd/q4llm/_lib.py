@@ -41,6 +41,7 @@ SIGNATURES = {
     "q4_linear": [p, i64, p, p, p, p, i64, i64, i32, p],
     "q4_linear_workspace_bytes": [i64, i64, C.POINTER(sz)],
     "q4_linear_ws": [p, i64, p, p, p, p, i64, i64, i32, p, sz, p],
+    "q4_linear_ws_split_bytes": [i64, i64, i64, i32, C.POINTER(sz)],
     "gemm_f16_nt": [p, p, p, i64, i64, i64, i64, i64, i64, p],
     "gemm_f16_nt_cfg": [p, p, p, i64, i64, i64, i64, i64, i64, i32, i32, p],
     "gemm_f16_num_configs": [],

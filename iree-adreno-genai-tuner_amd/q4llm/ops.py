@@ -162,8 +162,16 @@ def q4_linear(x, qweight, scales, group, residual=None, out=None):
     return out
 
 
-def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=None):
-    """q4_linear through the workspace entry point (x split once, multi-stage MFMA pipeline)."""
+def q4_linear_ws_split_bytes(m, n, k, group) -> int:
+    """Workspace bytes with which q4_linear_ws may split K for this shape (= the planes where it does not)."""
+    b = C.c_size_t(0)
+    LIB.call("q4_linear_ws_split_bytes", m, n, k, group, C.byref(b))
+    return b.value
+
+
+def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=None, split=False):
+    """q4_linear through the workspace entry point (x split once, multi-stage MFMA pipeline). With
+    split=True (and no workspace given) the workspace also holds the K-split partials."""
     n, k = _weights(qweight, scales, group)
     x = x.contiguous()
     _need(x, "x", torch.float32, (None, k))
@@ -177,7 +185,8 @@ def q4_linear_ws(x, qweight, scales, group, residual=None, out=None, workspace=N
     b = C.c_size_t(0)
     LIB.call("q4_linear_workspace_bytes", m, k, C.byref(b))
     if workspace is None:
-        workspace = torch.empty(b.value, dtype=torch.uint8, device=x.device)
+        need = q4_linear_ws_split_bytes(m, n, k, group) if split else b.value
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     LIB.call("q4_linear_ws", ptr(x), m, ptr(qweight), ptr(scales), ptr(out), ptr(residual), n, k, group,
              ptr(workspace), workspace.numel(), stream_of(x.device))
     return out

@@ -217,6 +217,45 @@ def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch)
     assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
 
 
+@pytest.mark.parametrize("M,N,K,group", [(256, 5120, 3072, 128), (256, 3072, 3072, 128), (256, 3072, 8192, 128),
+                                         (128, 5120, 3072, 128), (200, 3000, 3072, 128), (64, 256, 704, 64),
+                                         (16, 1408, 256, 32), (33, 520, 1024, 256), (256, 1000, 8192, 1024)])
+def test_q4_linear_ws_k_split(dev, M, N, K, group):
+    """With the larger workspace the prefill GEMM splits K over several workgroups per 64x256 tile and a
+    second kernel adds the partials (fixed order) and the residual: same accuracy as the unsplit form,
+    ragged M and N, split boundaries on group boundaries (group 256 and 1024: two and sixteen stages per
+    group), residual in place."""
+    from q4llm import ops as O
+    need = O.q4_linear_ws_split_bytes(M, N, K, group)
+    base = M * K * 4
+    assert need > base, "the shape should take a K split"
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g)
+    res = torch.randn(M, N, generator=g)
+    qw, sc = R.quantize_q4(w, group)
+    ref = x.double() @ R.dequantize_q4(qw, sc, group).double().T
+    rms = ref.pow(2).mean().sqrt().item()
+    xd, qd, sd = x.to(dev), qw.to(dev), sc.to(dev)
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)  # partials start as NaN bytes
+    y = nan_like((M, N), torch.float32, dev)
+    O.q4_linear_ws(xd, qd, sd, group, out=y, workspace=ws)
+    assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms
+    h = res.to(dev).clone()
+    O.q4_linear_ws(xd, qd, sd, group, residual=h, out=h, workspace=ws)
+    assert (h.cpu().double() - (ref + res.double())).abs().max().item() <= 1e-5 * (rms + 1)
+    # the split form agrees with the unsplit one to the fp32 rounding of a different summation order
+    y1 = O.q4_linear_ws(xd, qd, sd, group)
+    assert (y.cpu() - y1.cpu()).abs().max().item() <= 1e-5 * rms
+
+
+def test_q4_linear_ws_split_bytes_when_no_split(dev):
+    """Shapes whose tiles already fill the chip (and M > 256) need only the planes."""
+    from q4llm import ops as O
+    assert O.q4_linear_ws_split_bytes(256, 16384, 3072, 128) == 256 * 3072 * 4
+    assert O.q4_linear_ws_split_bytes(1024, 5120, 3072, 128) == 1024 * 3072 * 4
+
+
 # ------------------------------------------------------------------------------------------------
 # support ops
 # ------------------------------------------------------------------------------------------------
