@@ -20,10 +20,14 @@ namespace {
 // most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight; the
 // norm weights are loaded with them, so no memory round trip follows the row reduction.
 // With xh != nullptr the row goes to the fp16 (hi, lo) planes of a prefill projection instead of out.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+// With n_split > 0 (rows held in registers only) x is first completed with the K-split partials of the
+// projection that produced it, x += psum[0] + ... + psum[n_split - 1] (each [M, D]; the order of
+// linear_reduce_kernel, so the same bits), and the completed row is written back to x.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
                                                       const int32_t* __restrict__ row_sel,
-                                                      uint16_t* __restrict__ xh, uint16_t* __restrict__ xl) {
+                                                      uint16_t* __restrict__ xh, uint16_t* __restrict__ xl,
+                                                      const float* __restrict__ psum = nullptr, int n_split = 0) {
   // a selected row outside [0, M) is clamped (the reference's index_select would raise)
   const int64_t row = row_sel ? min(max(static_cast<int64_t>(row_sel[0]), int64_t{0}), M - 1) : blockIdx.x;
   const float* xr = x + row * D;
@@ -42,6 +46,26 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     for (int i = 0; i < kV; ++i) {
       const int64_t j = threadIdx.x + i * 256;
       wv[i] = j < D / 4 ? reinterpret_cast<const float4*>(w)[j] : make_float4(0, 0, 0, 0);
+    }
+    if (n_split > 0) {
+      const int64_t plane = M * D / 4;
+      const float4* pr = reinterpret_cast<const float4*>(psum) + row * (D / 4);
+#pragma unroll
+      for (int i = 0; i < kV; ++i) {
+        const int64_t j = threadIdx.x + i * 256;
+        if (j < D / 4) {
+          float4 a = pr[j];
+          for (int sp = 1; sp < n_split; ++sp) {
+            const float4 b = pr[sp * plane + j];
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+          }
+          v[i] = make_float4(v[i].x + a.x, v[i].y + a.y, v[i].z + a.z, v[i].w + a.w);
+          reinterpret_cast<float4*>(const_cast<float*>(xr))[j] = v[i];
+        }
+      }
     }
 #pragma unroll
     for (int i = 0; i < kV; ++i) {
@@ -140,10 +164,14 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qkv, c
 // The same for hd % 8 == 0 with four consecutive d per thread: 16-byte loads of the row halves and
 // the cos / sin entries, 16-byte row stores, 8-byte cache stores; the row loads are issued before
 // the position is known. Same expressions, so the same bits as rope_kv_kernel.
+// With n_split > 0 the rows are not read from qkv but summed from the K-split partials of the qkv
+// projection (part[s], each [C, (n_q + 2 n_kv) hd], in the order of linear_reduce_kernel); the rotated q
+// and k are written to qkv as usual (v only to the cache).
 __global__ __launch_bounds__(256) void rope_kv4_kernel(float* __restrict__ qkv, const float* __restrict__ cos_t,
                                                        const float* __restrict__ sin_t, uint16_t* __restrict__ kc,
                                                        uint16_t* __restrict__ vc, int C, int n_q, int n_kv, int hd,
-                                                       int max_ctx, const int32_t* __restrict__ start_p) {
+                                                       int max_ctx, const int32_t* __restrict__ start_p,
+                                                       const float* __restrict__ part = nullptr, int n_split = 0) {
   const int half = hd / 2, q4 = half / 4;
   const int heads = n_q + 2 * n_kv;
   const int64_t total = static_cast<int64_t>(C) * heads * q4;
@@ -153,8 +181,22 @@ __global__ __launch_bounds__(256) void rope_kv4_kernel(float* __restrict__ qkv, 
   const int head = static_cast<int>((t / q4) % heads);
   const int c = static_cast<int>(t / (static_cast<int64_t>(q4) * heads));
   float* row = qkv + (static_cast<int64_t>(c) * heads + head) * hd;
-  const float4 x1 = *reinterpret_cast<const float4*>(row + d);
-  const float4 x2 = *reinterpret_cast<const float4*>(row + d + half);
+  float4 x1, x2;
+  if (n_split > 0) {
+    const int64_t plane = static_cast<int64_t>(C) * heads * hd;
+    const float* pr = part + (row - qkv);
+    x1 = *reinterpret_cast<const float4*>(pr + d);
+    x2 = *reinterpret_cast<const float4*>(pr + d + half);
+    for (int sp = 1; sp < n_split; ++sp) {
+      const float4 b1 = *reinterpret_cast<const float4*>(pr + sp * plane + d);
+      const float4 b2 = *reinterpret_cast<const float4*>(pr + sp * plane + d + half);
+      x1 = make_float4(x1.x + b1.x, x1.y + b1.y, x1.z + b1.z, x1.w + b1.w);
+      x2 = make_float4(x2.x + b2.x, x2.y + b2.y, x2.z + b2.z, x2.w + b2.w);
+    }
+  } else {
+    x1 = *reinterpret_cast<const float4*>(row + d);
+    x2 = *reinterpret_cast<const float4*>(row + d + half);
+  }
   const int pos = start_p[0] + c;
   if (pos < 0 || pos >= max_ctx) return;
   auto half4 = [](float a, float b, float c4, float e) {
@@ -355,13 +397,43 @@ extern "C" int silu_mul_f32(const float* gu, float* out, int64_t M, int64_t inte
 
 namespace q4 {
 
-int rmsnorm_planes(const float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
-                   hipStream_t st) {
+bool rmsnorm_takes_partials(int64_t D) { return D % 4 == 0 && D <= 4 * 256 * 4; }
+
+int rmsnorm_planes(float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
+                   hipStream_t st, const float* part, int n_split) {
   if (!x || !w || !xh || !xl) return Q4_ERR_NULL;
   if (M <= 0 || D <= 0 || D % 8) return Q4_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
+  if (n_split > 0 && (!part || !aligned(part, 16) || !rmsnorm_takes_partials(D))) return Q4_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
-                     nullptr, xh, xl);
+                     nullptr, xh, xl, part, n_split);
+  return launch_status();
+}
+
+int rmsnorm_row_partials(float* x, const float* w, float* out, int64_t M, int64_t D, float eps, const int32_t* row,
+                         const float* part, int n_split, hipStream_t st) {
+  if (!x || !w || !out || !row || !part) return Q4_ERR_NULL;
+  if (M <= 0 || D <= 0 || n_split <= 0 || !rmsnorm_takes_partials(D)) return Q4_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || !aligned(part, 16)) return Q4_ERR_ALIGN;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, M, D, eps, row, nullptr, nullptr, part,
+                     n_split);
+  return launch_status();
+}
+
+bool rope_kv_takes_partials(const float* qkv, const float* cos_t, const float* sin_t, const uint16_t* kc,
+                            const uint16_t* vc, int hd) {
+  return hd % 8 == 0 && aligned(qkv, 16) && aligned(cos_t, 16) && aligned(sin_t, 16) && aligned(kc, 8) &&
+         aligned(vc, 8);
+}
+
+int rope_kv_partials(float* qkv, const float* part, int n_split, const float* cos_t, const float* sin_t, uint16_t* kc,
+                     uint16_t* vc, int C, int n_q, int n_kv, int hd, int max_ctx, const int32_t* start, hipStream_t st) {
+  if (!qkv || !part || !cos_t || !sin_t || !kc || !vc || !start) return Q4_ERR_NULL;
+  if (C <= 0 || n_q <= 0 || n_kv <= 0 || hd <= 0 || max_ctx <= 0 || n_split <= 0) return Q4_ERR_SHAPE;
+  if (!rope_kv_takes_partials(qkv, cos_t, sin_t, kc, vc, hd) || !aligned(part, 16)) return Q4_ERR_UNSUPPORTED;
+  const int64_t total = static_cast<int64_t>(C) * (n_q + 2 * n_kv) * (hd / 8);
+  hipLaunchKernelGGL(rope_kv4_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, st, qkv, cos_t,
+                     sin_t, kc, vc, C, n_q, n_kv, hd, max_ctx, start, part, n_split);
   return launch_status();
 }
 

@@ -60,17 +60,30 @@ size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group);
 
 // q4_linear_ws's GEMM on given planes (power-of-two group); with `part` (at least
 // linear_split_part_bytes, 16-byte aligned) it may split K and reduce the partials in a second kernel.
+// With `deferred` not null, a K split leaves its partials in `part` unreduced and sets *deferred to the
+// number of splits (0 when the result went to y); the caller's next kernel then completes y.
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st,
-                     float* part = nullptr, size_t part_bytes = 0);
+                     float* part = nullptr, size_t part_bytes = 0, int* deferred = nullptr);
 // The gate/up projection with silu(gate) * up written as the [M, N / 2] planes oh / ol (ol = oh + M N / 2)
 // of the down projection; Q4_ERR_UNSUPPORTED when the shape does not take the fused tile (the caller then
 // runs q4_linear_planes + silu_mul_planes).
 int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                             uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st);
-// rmsnorm_f32 of M rows (no row selection), written as planes.
-int rmsnorm_planes(const float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
-                   hipStream_t st);
+// rmsnorm_f32 of M rows (no row selection), written as planes. With n_split > 0 each row of x is first
+// completed with the K-split partials `part` of the projection that produced it (x += sum of n_split
+// [M, D] planes, written back to x); requires rmsnorm_takes_partials(D).
+bool rmsnorm_takes_partials(int64_t D);
+int rmsnorm_planes(float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t M, int64_t D, float eps,
+                   hipStream_t st, const float* part = nullptr, int n_split = 0);
+// rmsnorm_f32 of the selected row row[0] after completing it with the K-split partials (as above).
+int rmsnorm_row_partials(float* x, const float* w, float* out, int64_t M, int64_t D, float eps, const int32_t* row,
+                         const float* part, int n_split, hipStream_t st);
+// rope_kv_write with the qkv rows summed from the K-split partials of the qkv projection.
+bool rope_kv_takes_partials(const float* qkv, const float* cos_t, const float* sin_t, const uint16_t* kc,
+                            const uint16_t* vc, int hd);
+int rope_kv_partials(float* qkv, const float* part, int n_split, const float* cos_t, const float* sin_t, uint16_t* kc,
+                     uint16_t* vc, int C, int n_q, int n_kv, int hd, int max_ctx, const int32_t* start, hipStream_t st);
 // silu_mul_f32, written as planes.
 int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st);
 // attn_bucket for C > 1, its output written as planes.

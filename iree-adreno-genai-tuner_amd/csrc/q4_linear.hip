@@ -764,9 +764,10 @@ size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group) {
 // k-split tile while it gives at most 768 workgroups, else 64x64. Q4_LINEAR_CFG overrides (no K split).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st, float* part,
-                     size_t part_bytes) {
+                     size_t part_bytes, int* deferred) {
   if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
   if (!y) return Q4_ERR_NULL;
+  if (deferred) *deferred = 0;
   int ti = -1;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
@@ -785,6 +786,10 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
     hipLaunchKernelGGL(kLinWsFns[T], dim3(tiles * sp.n_split), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[T], st, xh,
                        xl, qw, sc, y, res, (int)M, (int)N, (int)K, group, tiles_n, sp.n_split, sp.nk_split, part);
     if (int e = launch_status()) return e;
+    if (deferred) {
+      *deferred = sp.n_split;
+      return Q4_OK;
+    }
     const int64_t n4 = M * N / 4;
     hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0, st,
                        reinterpret_cast<const float4*>(part), reinterpret_cast<const float4*>(res),

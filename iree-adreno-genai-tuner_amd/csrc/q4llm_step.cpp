@@ -195,6 +195,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   const bool use_t16 = fused && !getenv("Q4_NO_T16");
   auto has = [&](const q4llm_t16& t) { return use_t16 && t.tiles && t.scales; };
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
+  // K-split partials left by the last prefill projection for the kernel after it to add (0: none)
+  int pending = 0;
+  const bool defer_norm = planes && q4::rmsnorm_takes_partials(D);
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
     uint16_t* kc = static_cast<uint16_t*>(caches[2 * i]);
@@ -208,10 +211,18 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
         Q4_TRY(q4_gemv_epilogue(ly.wqkv_q, ly.wqkv_s, h, Q4_PRO_RMSNORM, ly.ln_in, m->eps, Q4_EPI_ROPE_KV, &rope, qkv,
                                 qkv_w, D, m->group, stream));
     } else if (planes) {
-      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st));
+      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st, part, pending));
+      pending = 0;
+      // the qkv partials are added by the RoPE + KV-write kernel
+      const bool defer_rope = q4::rope_kv_takes_partials(qkv, m->cos_t, m->sin_t, kc, vc, hd);
+      int qkv_split = 0;
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st, part,
-                                  lo.part_bytes));
-      Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
+                                  lo.part_bytes, defer_rope ? &qkv_split : nullptr));
+      if (qkv_split > 0)
+        Q4_TRY(q4::rope_kv_partials(qkv, part, qkv_split, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start,
+                                    st));
+      else
+        Q4_TRY(rope_kv_write(qkv, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start, stream));
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_in, x, C, D, m->eps, nullptr, stream));
       Q4_TRY(proj(C, x, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, lin_ws, lo.lin_bytes, stream));
@@ -220,7 +231,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
     if (planes) {
       Q4_TRY(q4::attn_bucket_planes(qkv, qkv_w, kc, vc, xh, xl, C, nh, nkv, hd, L, start, scale, attn_ws,
                                     lo.attn_bytes, st));
-      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st, part, lo.part_bytes));
+      // the o-projection's partials are added to h by the post-attention norm
+      Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st, part, lo.part_bytes,
+                                  defer_norm ? &pending : nullptr));
     } else {
       Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
       if (has(ly.wo_t))
@@ -242,22 +255,24 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       else
         Q4_TRY(q4_gemv(ly.wdown_q, ly.wdown_s, act, Q4_F32, h, Q4_F32, h, D, m->inter, m->group, stream));
     } else if (planes) {
-      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_post, xh, xl, C, D, m->eps, st));
+      Q4_TRY(q4::rmsnorm_planes(h, ly.ln_post, xh, xl, C, D, m->eps, st, part, pending));
+      pending = 0;
       // gate/up + SwiGLU in one kernel where the shape takes it (its planes go to the gu buffer, which
       // holds the [C, 2 inter] fp32 otherwise), else the GEMM and silu_mul as two kernels
       uint16_t* ah = reinterpret_cast<uint16_t*>(gu);
       uint16_t* al = ah + static_cast<int64_t>(C) * m->inter;
       const int fused = q4::q4_linear_planes_swiglu(xh, xl, C, ly.wgu_q, ly.wgu_s, ah, al, 2 * m->inter, D, m->group, st);
+      // the down projection's partials are added to h by the next layer's input norm (or the final norm)
       if (fused == Q4_OK) {
         Q4_TRY(q4::q4_linear_planes(ah, al, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
-                                    lo.part_bytes));
+                                    lo.part_bytes, defer_norm ? &pending : nullptr));
       } else {
         if (fused != Q4_ERR_UNSUPPORTED) return fused;
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st, part,
                                     lo.part_bytes));
         Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
-                                    lo.part_bytes));
+                                    lo.part_bytes, defer_norm ? &pending : nullptr));
       }
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));
@@ -280,6 +295,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   if (fused) {  // one row: the final norm is the LM head's prologue
     Q4_TRY(q4_gemv_fused(m->embed_q, m->embed_s, h, Q4_PRO_RMSNORM, m->ln_f, m->eps, lg, nullptr, m->vocab, D,
                          m->group, stream));
+  } else if (pending > 0) {
+    Q4_TRY(q4::rmsnorm_row_partials(h, m->ln_f, xf, C, D, m->eps, last, part, pending, st));
+    Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
   } else {
     Q4_TRY(rmsnorm_f32(h, m->ln_f, xf, C, D, m->eps, last, stream));
     Q4_TRY(q4_gemv(m->embed_q, m->embed_s, xf, Q4_F32, lg, Q4_F32, nullptr, m->vocab, D, m->group, stream));
