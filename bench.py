@@ -45,13 +45,13 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 2 ** 20
 
 # HBM bytes per 5120x3072 launch from rocprofv3 counter passes over this bench's GEMV leg
-# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4020.0 KiB x 1.995 (the factor that maps
-# FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 20.0 KiB x 1.0.
+# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4025.0 KiB x 1.99497 (the factor that maps
+# FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 24.0 KiB x 1.0.
 # Counters cannot be read inside a timed run, so the figure is carried here with its source.
-GEMV_TRAFFIC_BYTES_5120x3072 = 8_232_858
+GEMV_TRAFFIC_BYTES_5120x3072 = 8_247_054
 # Average kernel duration of the 5120x3072 launch in the rocprofv3 kernel trace of this bench's GEMV
 # leg (profiles/q4_gemv_5120x3072_kernel_stats.md); reported beside the live HIP-event figure.
-GEMV_ROCPROF_AVG_US = 3.486
+GEMV_ROCPROF_AVG_US = 3.746
 
 
 def log(*a):

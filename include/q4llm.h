@@ -287,8 +287,8 @@ int q4llm_step(const q4llm_model* m, const int32_t* tokens, int C, const int32_t
                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Size of the per-GPU scratch array of q4llm_step_noalloc: 64 MiB. That covers every decode step
- * (C == 1; the Llama-3.2-3B shape needs 1.03 MiB) and prefill chunks up to that size (3B shape:
- * C = 256 at L <= 512 needs 58.7 MiB; q4llm_step_workspace_bytes gives the figure for a shape). */
+ * (C == 1; the Llama-3.2-3B shape needs 1.15 MiB) and prefill chunks up to that size (3B shape:
+ * C = 256 at L <= 512 needs 61.6 MiB; q4llm_step_workspace_bytes gives the figure for a shape). */
 #define Q4LLM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* q4llm_step without a workspace argument and without any allocation. No counterpart in the

@@ -18,7 +18,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <array>
 #include <cmath>
 #include <cstddef>
 #include <cstdlib>
@@ -60,7 +59,20 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   lo->act = take(f * C * m->inter);
   lo->xf = take(f * m->dim);
   lo->logits = take(f * m->vocab);
-  lo->attn = take(attn);
+  // K-split partials of the prefill projections (the largest of the four). They share their region with
+  // the attention workspace: the qkv partials are added (by RoPE + KV write) before the attention runs,
+  // and the o and down partials are written after it and added (by the next rms_norm) before the next.
+  size_t part = 0;
+  if (C > 1) {
+    const int64_t shapes[4][2] = {{nq + 2 * nkv, m->dim}, {m->dim, nq}, {2 * static_cast<int64_t>(m->inter), m->dim},
+                                  {m->dim, m->inter}};
+    for (const auto& nk : shapes)
+      if (linear_fits(static_cast<int>(nk[1]), m->group) && (m->group & (m->group - 1)) == 0)
+        part = std::max(part, q4::linear_split_part_bytes(C, nk[0], nk[1], m->group));
+  }
+  lo->attn = take(std::max(attn, part));
+  lo->part = lo->attn;
+  lo->part_bytes = part;
   lo->amax = take(amax);
   lo->attn_bytes = attn;
   lo->amax_bytes = amax;
@@ -75,17 +87,6 @@ int layout_for(const q4llm_model* m, int C, int L, Layout* lo) {
   }
   lo->lin = take(lin);
   lo->lin_bytes = lin;
-  // K-split partials of the prefill projections (the largest of the four)
-  size_t part = 0;
-  if (C > 1) {
-    for (const int64_t* nk : {std::array<int64_t, 2>{nq + 2 * nkv, m->dim}.data(), std::array<int64_t, 2>{m->dim, nq}.data(),
-                              std::array<int64_t, 2>{2 * static_cast<int64_t>(m->inter), m->dim}.data(),
-                              std::array<int64_t, 2>{m->dim, m->inter}.data()})
-      if (linear_fits(static_cast<int>(nk[1]), m->group) && (m->group & (m->group - 1)) == 0)
-        part = std::max(part, q4::linear_split_part_bytes(C, nk[0], nk[1], m->group));
-  }
-  lo->part = take(part);
-  lo->part_bytes = part;
   lo->total = off;
   return Q4_OK;
 }
