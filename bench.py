@@ -279,8 +279,10 @@ GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 
 
 
 def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
-    """Config 3. Parity against the host fp32 matmul of the same fp16 inputs (gemm/shapes.py:62), whose
-    wall time on this host's cores is the leg's CPU figure; error is max|C - ref| / rms(ref)."""
+    """Config 3 through gemm_f16_nt_ws (the 256-row shapes split K over a workspace allocated once per
+    shape, outside the timed region). Parity against the host fp32 matmul of the same fp16 inputs
+    (gemm/shapes.py:62), whose wall time on this host's cores is the leg's CPU figure; error is
+    max|C - ref| / rms(ref)."""
     import torch
     from q4llm import ops, synth
     cores = cpu_threads()
@@ -293,7 +295,8 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
         Bs = [B0.clone() for _ in range(nb)]
         C = torch.empty(M, N, dtype=torch.float16, device=dev)
         C.fill_(float("nan"))
-        ops.gemm_f16_nt(A, B0, out=C)
+        ws = torch.empty(max(ops.gemm_f16_nt_ws_bytes(M, N, K), 16), dtype=torch.uint8, device=dev)
+        ops.gemm_f16_nt_ws(A, B0, out=C, workspace=ws)
         got = C.cpu().float()
         a32, b32 = torch.from_numpy(a).float(), torch.from_numpy(b).float()
         ref_box = {}
@@ -305,7 +308,7 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
         ref = ref_box["r"]
         err = (got - ref).abs().max().item() / ref.pow(2).mean().sqrt().item()
         del ref, ref_box, got
-        fns = [lambda B=B: ops.gemm_f16_nt(A, B, out=C) for B in Bs]
+        fns = [lambda B=B: ops.gemm_f16_nt_ws(A, B, out=C, workspace=ws) for B in Bs]
         st = stats_us(timed_steps(fns, max(16, len(fns) * 2), len(fns), reps))
         ms = st["median"] / 1e3
         flops = 2.0 * M * N * K
@@ -320,7 +323,7 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
                                "cpu_cores": cores, "cpu_reps": cpu_n}
         log(f"gemm {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}) {tf:.1f} TFLOP/s "
             f"({tf / attain:.1%} of attainable {attain:.0f}); host fp32 {cpu_ms:.2f} ms; err/rms {err:.2e}")
-        del A, B0, Bs, C
+        del A, B0, Bs, C, ws
         torch.cuda.empty_cache()
     return out
 

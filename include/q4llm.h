@@ -190,6 +190,21 @@ int q4_linear_ws(const float* x, int64_t M, const int32_t* qweight, const uint16
 int gemm_f16_nt(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, void* stream);
 
+/* Bytes of device workspace gemm_f16_nt_ws needs for an M x N x K problem (0: it does not split K
+ * for this shape). */
+int gemm_f16_nt_ws_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
+/* gemm_f16_nt with a caller-provided device workspace (16-byte aligned, at least
+ * gemm_f16_nt_ws_bytes bytes; it may be NULL when that query gives 0): for shapes whose output tiles
+ * alone leave CUs idle, K is split over several workgroups per tile, each writing an fp32 partial
+ * into the workspace, and a second launch adds the partials in a fixed order and writes C, so the
+ * result does not depend on timing. Same argument rules and result tolerance as gemm_f16_nt;
+ * Q4_ERR_WORKSPACE when the workspace is missing or too small. Replaces the same call of the
+ * reference's harness (gemm/harness/vk_gemm_bench.c dispatch of one NT problem) where the caller
+ * can hold a workspace. */
+int gemm_f16_nt_ws(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Attention over a KV bucket (reference: LlamaQ4.step, llama_q4.py:204-232)
  * ------------------------------------------------------------------------------------------- */
@@ -349,7 +364,8 @@ int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
  *   q4_gemv_config_info:    lanes per row, chunks per lane, rows per lane, waves, x words, grid-stride
  *   q4_gemv_mx_config_info: row blocks per workgroup, waves per row block, tiles per wave, used rows
  *                           per 16-row block, grid-stride (q4_gemv_mx_num_configs entries)
- *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, ping-pong
+ *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, ping-pong, pipelined
+ *                           substeps (8 ints)
  *   q4_linear_ws_config_info: BM, BN, wave rows, wave columns, stages, k-split */
 int q4_gemv_config_info(int cfg, int* info);
 int q4_gemv_mx_num_configs(void);

@@ -26,7 +26,9 @@
 // (row 8 * (j / 4) + 4 * (l / 32) + j % 4, col l % 32).
 #include "q4_common.h"
 
+#include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace q4 {
 namespace {
@@ -47,10 +49,11 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 }
 
 // 16 bytes per lane from global memory straight into LDS: lane i's bytes land at dst + 16 i (dst
-// is wave-uniform). Out-of-range offsets land zeros.
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off) {
+// is wave-uniform). Out-of-range offsets land zeros; `soff` (a uniform addend) is used only where
+// the whole access is in range.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off, uint32_t soff = 0) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst), 16, off,
-                                           0, 0, 0);
+                                           static_cast<int>(soff), 0, 0);
 }
 
 // s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt left at their maxima).
@@ -71,11 +74,14 @@ struct GemmCfg {
   static constexpr int kRow = BK * 2;                  // bytes per LDS row: 128 (BK 64) or 64 (BK 32)
   static constexpr int kRowsPerInst = 1024 / kRow;     // rows one direct-load instruction fills
   static constexpr int kStage = (BM + BN) * kRow;
-  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + 1024;  // + junk for spare loads
   // direct-load instructions per wave and stage; when the waves do not divide the row blocks, the spare
-  // instructions load nothing into the junk area, so every wave issues the same number per stage
+  // instructions load nothing into a 1 KB junk area after the stages, so every wave issues the same
+  // number per stage
   static constexpr int kAI = (BM / kRowsPerInst + kWaves - 1) / kWaves;
   static constexpr int kBI = (BN / kRowsPerInst + kWaves - 1) / kWaves;
+  static constexpr bool kJunk = (BM / kRowsPerInst) % kWaves != 0 || (BN / kRowsPerInst) % kWaves != 0;
+  static constexpr size_t kLds = static_cast<size_t>(NST) * kStage + (kJunk ? 1024 : 0);
+  static_assert(kLds <= 160 * 1024, "LDS per workgroup");
   static constexpr int kLPW = kAI + kBI;
   static_assert(BK == 32 || BK == 64, "K step");
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 MFMA tile");
@@ -94,19 +100,39 @@ __device__ __forceinline__ int swz(int r) {
   return BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3;
 }
 
-template <int BM, int BN, int WM, int WN, int NST, int BK>
+// Wait until this wave has at most `after` stages of kLPW direct loads in flight (after <= MAXA;
+// vector-memory loads complete in issue order).
+template <int LPW, int MAXA>
+__device__ __forceinline__ void wait_stages(int after) {
+  static_assert(MAXA * LPW < 64, "vmcnt holds at most 63 loads");
+  if constexpr (MAXA >= 3)
+    if (after >= 3) return wait_vmcnt<3 * LPW>();
+  if constexpr (MAXA >= 2)
+    if (after >= 2) return wait_vmcnt<2 * LPW>();
+  if constexpr (MAXA >= 1)
+    if (after >= 1) return wait_vmcnt<LPW>();
+  wait_vmcnt<0>();
+}
+
+template <int BM, int BN, int WM, int WN, int NST, int BK, bool PIPE>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ Cm, int M, int N, int K,
-    int lda, int ldb, int ldc, int tiles_m, int tiles_n, int xcd_remap) {
+    int lda, int ldb, int ldc, int tiles_m, int tiles_n, int xcd_remap, int n_split, int nk_split,
+    float* __restrict__ P) {
   using G = GemmCfg<BM, BN, WM, WN, NST, BK>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
 
   // XCD-major tile order: workgroup b runs on XCD b % 8; give XCD x a contiguous range of the
   // tile sequence. The sequence walks groups of kGroupM tile rows column by column, so the range an
   // XCD holds is a compact block (4 x 8 tiles for 32 tiles) whose A and B panels stay in its L2.
-  int bid = blockIdx.x;
+  // With a K split (n_split > 1) the sequence is the tile sequence once per K range: workgroup
+  // g of the sequence computes K range g / ntiles of tile g % ntiles, so an XCD's block shares its
+  // K range and reuses its panel slices the same way.
+  int g = blockIdx.x;
   const int ntiles = tiles_m * tiles_n;
-  if (xcd_remap) bid = (bid % 8) * (ntiles / 8) + bid / 8;
+  if (xcd_remap) g = (g % 8) * (static_cast<int>(gridDim.x) / 8) + g / 8;
+  const int ksp = g / ntiles;
+  const int bid = g - ksp * ntiles;
   constexpr int kGroupM = 4;
   const int group = bid / (kGroupM * tiles_n);
   const int first_m = group * kGroupM;
@@ -124,40 +150,47 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
 
   // Direct loads: instruction j of this wave fills row block b = wave + j * kWaves (kRowsPerInst
   // rows) of the stage; the lane for LDS slot s = lane % (BK / 8) of tile row
-  // r = b * kRowsPerInst + lane / (BK / 8) fetches chunk s ^ swz(r).
+  // r = b * kRowsPerInst + lane / (BK / 8) fetches chunk s ^ swz(r). With an even number of waves
+  // (or BK 32) swz(r) does not depend on j, so one per-lane offset per operand serves every
+  // instruction: instruction j adds j row blocks of the wave stride, a uniform value that full
+  // tiles pass as the load's scalar offset (no per-load vector arithmetic or registers).
+  static_assert(BK == 32 || G::kWaves % 2 == 0, "the lane's chunk is the same for every row block");
   constexpr int kCpr = BK / 8;  // chunks per row
-  uint32_t aoff[G::kAI], boff[G::kBI];
-  int achunk[G::kAI], bchunk[G::kBI];
-  bool areal[G::kAI], breal[G::kBI];
-#pragma unroll
-  for (int j = 0; j < G::kAI; ++j) {
-    const int b = wave + j * G::kWaves;
-    const int r = b * G::kRowsPerInst + lane / kCpr;
-    areal[j] = b < BM / G::kRowsPerInst;
-    achunk[j] = (lane % kCpr) ^ swz<BK>(r);
-    aoff[j] = areal[j] && m0 + r < M ? static_cast<uint32_t>(m0 + r) * lda * 2u + achunk[j] * 16u : kOOB;
-  }
-#pragma unroll
-  for (int j = 0; j < G::kBI; ++j) {
-    const int b = wave + j * G::kWaves;
-    const int r = b * G::kRowsPerInst + lane / kCpr;
-    breal[j] = b < BN / G::kRowsPerInst;
-    bchunk[j] = (lane % kCpr) ^ swz<BK>(r);
-    boff[j] = breal[j] && n0 + r < N ? static_cast<uint32_t>(n0 + r) * ldb * 2u + bchunk[j] * 16u : kOOB;
-  }
+  constexpr int kRowsPerJ = G::kWaves * G::kRowsPerInst;
+  const int r0 = wave * G::kRowsPerInst + lane / kCpr;
+  const int chunk = (lane % kCpr) ^ swz<BK>(r0);
+  const uint32_t a_lane = static_cast<uint32_t>(m0 + r0) * lda * 2u + chunk * 16u;
+  const uint32_t b_lane = static_cast<uint32_t>(n0 + r0) * ldb * 2u + chunk * 16u;
+  const uint32_t a_step = static_cast<uint32_t>(kRowsPerJ) * lda * 2u;
+  const uint32_t b_step = static_cast<uint32_t>(kRowsPerJ) * ldb * 2u;
+  const int a_left = M - m0 - r0, b_left = N - n0 - r0;  // in-range rows from this lane's first row
+  const bool full_tile = m0 + BM <= M && n0 + BN <= N;
   unsigned char* junk = lds + NST * G::kStage;
   auto issue = [&](int kt, int stage) {
     const int k0 = kt * BK;
     unsigned char* sa = lds + stage * G::kStage;
     unsigned char* sb = sa + BM * G::kRow;
+    auto dst = [&](unsigned char* base, int j, int blocks) {
+      return wave + j * G::kWaves < blocks ? base + (wave + j * G::kWaves) * 1024 : junk;
+    };
+    if (full_tile && k0 + BK <= K) {
+      const uint32_t ao = a_lane + k0 * 2u, bo = b_lane + k0 * 2u;
 #pragma unroll
-    for (int j = 0; j < G::kAI; ++j)
-      load_lds16(ar, areal[j] ? sa + (wave + j * G::kWaves) * 1024 : junk,
-                 k0 + 8 * achunk[j] < K && aoff[j] != kOOB ? aoff[j] + k0 * 2u : kOOB);
+      for (int j = 0; j < G::kAI; ++j) load_lds16(ar, dst(sa, j, BM / G::kRowsPerInst), ao, j * a_step);
 #pragma unroll
-    for (int j = 0; j < G::kBI; ++j)
-      load_lds16(br, breal[j] ? sb + (wave + j * G::kWaves) * 1024 : junk,
-                 k0 + 8 * bchunk[j] < K && boff[j] != kOOB ? boff[j] + k0 * 2u : kOOB);
+      for (int j = 0; j < G::kBI; ++j) load_lds16(br, dst(sb, j, BN / G::kRowsPerInst), bo, j * b_step);
+    } else {
+      // edge tile or ragged last K step: rows past M / N and k past K read out of range (zeros)
+      const bool kin = k0 + 8 * chunk < K;
+#pragma unroll
+      for (int j = 0; j < G::kAI; ++j)
+        load_lds16(ar, dst(sa, j, BM / G::kRowsPerInst),
+                   kin && j * kRowsPerJ < a_left ? a_lane + j * a_step + k0 * 2u : kOOB);
+#pragma unroll
+      for (int j = 0; j < G::kBI; ++j)
+        load_lds16(br, dst(sb, j, BN / G::kRowsPerInst),
+                   kin && j * kRowsPerJ < b_left ? b_lane + j * b_step + k0 * 2u : kOOB);
+    }
   };
 
   float16v acc[G::TM][G::TN];
@@ -197,24 +230,130 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
   };
 
-  const int nk = (K + BK - 1) / BK;
+  // K steps [kt0, kt0 + nk) of this workgroup: all of them, or K range ksp of a K split.
+  const int nk_all = (K + BK - 1) / BK;
+  const int kt0 = n_split > 1 ? ksp * nk_split : 0;
+  const int nk = n_split > 1 ? min(nk_split, nk_all - kt0) : nk_all;
+  auto barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  if constexpr (!PIPE) {
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    // This wave's loads of stage kt are complete once at most `after` later stages are in flight.
-    const int after = min(NST - 2, nk - 1 - kt);
-    if (after >= 2) wait_vmcnt<(NST >= 4 ? 2 * G::kLPW : 0)>();
-    else if (after == 1) wait_vmcnt<(NST >= 3 ? G::kLPW : 0)>();
-    else wait_vmcnt<0>();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();  // every wave's stage-kt loads landed; stage kt-1 is no longer read
-    asm volatile("" ::: "memory");
-    if (kt + NST - 1 < nk) issue(kt + NST - 1, (kt + NST - 1) % NST);
-    compute(kt % NST);
+    for (int s = 0; s < NST - 1; ++s)
+      if (s < nk) issue(kt0 + s, s);
+    for (int kt = 0; kt < nk; ++kt) {
+      // This wave's loads of stage kt are complete once at most `after` later stages are in flight.
+      wait_stages<G::kLPW, NST - 2>(min(NST - 2, nk - 1 - kt));
+      barrier();  // every wave's stage-kt loads landed; stage kt-1 is no longer read
+      if (kt + NST - 1 < nk) issue(kt0 + kt + NST - 1, (kt + NST - 1) % NST);
+      compute(kt % NST);
+    }
+  } else {
+    // Software pipeline: the operands of each 16-k substep are read into one of two fragment sets
+    // while the MFMAs of the previous substep run from the other, so the LDS reads overlap the matrix
+    // core instead of preceding it. All NST stages are prefetched; the one barrier per K step sits
+    // after this wave's reads of the step (and before its last MFMAs): past it every wave is done
+    // reading stage kt, whose buffer then takes stage kt + NST, and stage kt + 1 has landed, whose
+    // first substep is read while the last MFMAs of step kt run. The direct loads of stage kt + NST
+    // are spread over the first KK - 1 substeps of step kt + 1, one between MFMAs, so the wait for the
+    // load queue overlaps the matrix core; they are all issued before the next boundary, which keeps
+    // its vmcnt count exact (and, with two stages, issues the stage it waits for).
+    constexpr int KK = BK / 16;
+    static_assert(KK % 2 == 0, "the last substep of a step uses fragment set 1");
+    half8 fa[2][G::TM], fb[2][G::TN];
+    auto read_sub = [&](int stage, int kk, int set) {
+      const unsigned char* sa = lds + stage * G::kStage;
+      const unsigned char* sb = sa + BM * G::kRow;
+      const int sw = ((2 * kk + (lane >> 5)) ^ swz<BK>(lane & 31)) << 4;
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i) fa[set][i] = *reinterpret_cast<const half8*>(sa + (arow + 32 * i) * G::kRow + sw);
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) fb[set][j] = *reinterpret_cast<const half8*>(sb + (brow + 32 * j) * G::kRow + sw);
+    };
+    // Loads of this workgroup's K step kl (K steps kt0 + kl, buffer kl % NST) given to substep
+    // q < KK - 1: A loads [q kAI / (KK - 1), (q + 1) kAI / (KK - 1)), B loads likewise. kFast: a full
+    // tile and a whole K step (offsets need no range checks).
+    auto issue_part = [&](auto fast, int kl, int q) {
+      constexpr bool kFast = decltype(fast)::value;
+      const int k0 = (kt0 + kl) * BK;
+      unsigned char* sa = lds + (kl % NST) * G::kStage;
+      unsigned char* sb = sa + BM * G::kRow;
+      auto dst = [&](unsigned char* base, int j, int blocks) {
+        return wave + j * G::kWaves < blocks ? base + (wave + j * G::kWaves) * 1024 : junk;
+      };
+      const bool kin = kFast || k0 + 8 * chunk < K;
+#pragma unroll
+      for (int j = q * G::kAI / (KK - 1); j < (q + 1) * G::kAI / (KK - 1); ++j) {
+        if constexpr (kFast) load_lds16(ar, dst(sa, j, BM / G::kRowsPerInst), a_lane + k0 * 2u, j * a_step);
+        else load_lds16(ar, dst(sa, j, BM / G::kRowsPerInst), kin && j * kRowsPerJ < a_left ? a_lane + j * a_step + k0 * 2u : kOOB);
+      }
+#pragma unroll
+      for (int j = q * G::kBI / (KK - 1); j < (q + 1) * G::kBI / (KK - 1); ++j) {
+        if constexpr (kFast) load_lds16(br, dst(sb, j, BN / G::kRowsPerInst), b_lane + k0 * 2u, j * b_step);
+        else load_lds16(br, dst(sb, j, BN / G::kRowsPerInst), kin && j * kRowsPerJ < b_left ? b_lane + j * b_step + k0 * 2u : kOOB);
+      }
+    };
+    // MFMAs of one substep with that substep's share of the loads interleaved (one load after each
+    // of the first MFMAs).
+    auto mfma_sub = [&](int set, auto fast, int kl, int q) {
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+      if (kl >= 0) issue_part(fast, kl, q);
+      constexpr int kLoads = (G::kAI + G::kBI + KK - 2) / (KK - 1);
+#pragma unroll
+      for (int l = 0; l < kLoads && l < G::TM * G::TN; ++l) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one vector-memory load
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, G::TM * G::TN, 0);
+    };
+    auto main_loop = [&](auto fast) {
+#pragma unroll
+      for (int s = 0; s < NST; ++s)
+        if (s < nk) {
+#pragma unroll
+          for (int q = 0; q < KK - 1; ++q) issue_part(std::false_type{}, s, q);
+        }
+      wait_stages<G::kLPW, NST - 1>(min(NST - 1, nk - 1));
+      barrier();
+      read_sub(0, 0, 0);
+      for (int kt = 0; kt < nk; ++kt) {
+        const int st = kt % NST;
+        // stage kt - 1 + NST goes into the buffer freed at the last boundary (none in step 0)
+        const int kl = kt >= 1 && kt - 1 + NST < nk ? kt - 1 + NST : -1;
+#pragma unroll
+        for (int kk = 0; kk < KK - 1; ++kk) {
+          read_sub(st, kk + 1, (kk + 1) & 1);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_sub(kk & 1, fast, kl, kk);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (kt + 1 < nk) {
+          // this wave's stage kt + 1 loads landed (stages up to kt - 1 + NST issued)
+          wait_stages<G::kLPW, NST - 2>(min(NST - 2, nk - kt - 2));
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage kt done
+          barrier();
+          read_sub((kt + 1) % NST, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_sub((KK - 1) & 1, fast, -1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    // the prologue's loads take the checked path (they are few); the loop's are checked only for
+    // edge tiles and a ragged K
+    if (full_tile && K % BK == 0) main_loop(std::true_type{});
+    else main_loop(std::false_type{});
   }
 
-  // Epilogue: fp16 stores (lane l holds column l % 32 of each 32x32 tile).
+  // Epilogue (lane l holds column l % 32 of each 32x32 tile): fp16 stores, or with a K split the
+  // fp32 partial of K range ksp into P[ksp][M][N].
+  float* __restrict__ Pk = P + static_cast<int64_t>(ksp) * M * N;
 #pragma unroll
   for (int i = 0; i < G::TM; ++i)
 #pragma unroll
@@ -223,8 +362,42 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_nt_kernel(
       for (int e = 0; e < 16; ++e) {
         const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
         const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
-        if (row < M && col < N) Cm[static_cast<int64_t>(row) * ldc + col] = float_to_half_bits(acc[i][j][e]);
+        if (row < M && col < N) {
+          if (n_split > 1) Pk[static_cast<int64_t>(row) * N + col] = acc[i][j][e];
+          else Cm[static_cast<int64_t>(row) * ldc + col] = float_to_half_bits(acc[i][j][e]);
+        }
       }
+}
+
+// C = fp16(sum over s of P[s]) for a K split: four consecutive outputs per thread (N % 4 == 0), the
+// partials added in the fixed order s = 0, 1, ..., n_split - 1, so results do not depend on which
+// workgroup finished first. kPacked: one 8-byte store per thread (ldc % 4 == 0, C 8-byte aligned).
+template <bool kPacked>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ P, uint16_t* __restrict__ Cm,
+                                                                int M, int N, int ldc, int n_split) {
+  const int64_t mn = static_cast<int64_t>(M) * N;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  float4 v = *reinterpret_cast<const float4*>(P + i);
+#pragma unroll 4
+  for (int s = 1; s < n_split; ++s) {
+    const float4 p = *reinterpret_cast<const float4*>(P + s * mn + i);
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  const int row = static_cast<int>(i / N), col = static_cast<int>(i - static_cast<int64_t>(row) * N);
+  uint16_t* c = Cm + static_cast<int64_t>(row) * ldc + col;
+  if (kPacked) {
+    *reinterpret_cast<uint2*>(c) = make_uint2(float_to_half_bits(v.x) | (uint32_t{float_to_half_bits(v.y)} << 16),
+                                              float_to_half_bits(v.z) | (uint32_t{float_to_half_bits(v.w)} << 16));
+  } else {
+    c[0] = float_to_half_bits(v.x);
+    c[1] = float_to_half_bits(v.y);
+    c[2] = float_to_half_bits(v.z);
+    c[3] = float_to_half_bits(v.w);
+  }
 }
 
 // Ping-pong variant of the kernel above for 8 waves (WM = 2, WN = 4) and an NST-stage ring.
@@ -253,7 +426,8 @@ template <int BM, int BN, int NST, int BK>
 __global__ __launch_bounds__(512) void gemm_f16_nt_pp_kernel(const uint16_t* __restrict__ A,
                                                               const uint16_t* __restrict__ B, uint16_t* __restrict__ Cm,
                                                               int M, int N, int K, int lda, int ldb, int ldc,
-                                                              int tiles_m, int tiles_n, int xcd_remap) {
+                                                              int tiles_m, int tiles_n, int xcd_remap, int, int,
+                                                              float*) {  // no K split
   constexpr int WM = 2, WN = 4;
   using G = GemmCfg<BM, BN, WM, WN, NST, BK>;
   static_assert(G::kLPW * (NST - 1) < 64, "vmcnt holds at most 63 loads");
@@ -441,7 +615,8 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
 
 struct TileCfg {
   int bm, bn, wgm, wgn, nst, bk;
-  bool pp;  // ping-pong schedule (gemm_f16_nt_pp_kernel: 8 waves as 2 x 4)
+  bool pp = false;  // ping-pong schedule (gemm_f16_nt_pp_kernel: 8 waves as 2 x 4)
+  bool sp = false;  // software-pipelined substeps (gemm_f16_nt_kernel<..., true>)
 };
 // Explicit CDNA4 tile list (index stable for gemm_f16_nt_cfg / Q4_GEMM_CFG).
 constexpr TileCfg kTiles[] = {
@@ -456,10 +631,13 @@ constexpr TileCfg kTiles[] = {
     {256, 256, 2, 4, 4, 32, true},  // 8: ping-pong, 4 stages of K 32 (128 KB)
     {256, 128, 2, 4, 3, 64, true},  // 9: 8 waves of 128x32, ping-pong, 3 stages (144 KB)
     {64, 96, 2, 3, 4, 64},          // 10: 6 waves of 32x32, 4 stages (81 KB): M = 256, N = 5120 on 216 CUs
+    {128, 128, 2, 2, 4, 64, false, true},  // 11: entry 3 with software-pipelined substeps
+    {64, 96, 2, 3, 4, 64, false, true},    // 12: entry 10 with software-pipelined substeps
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-using GemmFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int, int, int, int);
+using GemmFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, int, int, int, int, int,
+                        int, float*);
 
 template <int I>
 constexpr GemmFn gemm_fn() {
@@ -468,7 +646,7 @@ constexpr GemmFn gemm_fn() {
     static_assert(t.wgm == 2 && t.wgn == 4, "ping-pong entries are 2 x 4 waves");
     return gemm_f16_nt_pp_kernel<t.bm, t.bn, t.nst, t.bk>;
   } else {
-    return gemm_f16_nt_kernel<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>;
+    return gemm_f16_nt_kernel<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.sp>;
   }
 }
 template <int I>
@@ -476,22 +654,29 @@ constexpr size_t gemm_lds() {
   constexpr TileCfg t = kTiles[I];
   return GemmCfg<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>::kLds;
 }
-constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>(), gemm_fn<5>(),
-                               gemm_fn<6>(), gemm_fn<7>(), gemm_fn<8>(), gemm_fn<9>(), gemm_fn<10>()};
-constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(), gemm_lds<4>(), gemm_lds<5>(),
-                               gemm_lds<6>(), gemm_lds<7>(), gemm_lds<8>(), gemm_lds<9>(), gemm_lds<10>()};
+constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>(),
+                               gemm_fn<5>(), gemm_fn<6>(), gemm_fn<7>(), gemm_fn<8>(), gemm_fn<9>(),
+                               gemm_fn<10>(), gemm_fn<11>(), gemm_fn<12>()};
+constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(), gemm_lds<4>(),
+                               gemm_lds<5>(), gemm_lds<6>(), gemm_lds<7>(), gemm_lds<8>(), gemm_lds<9>(),
+                               gemm_lds<10>(), gemm_lds<11>(), gemm_lds<12>()};
 static_assert(sizeof(kGemmFns) / sizeof(kGemmFns[0]) == kNumTiles, "one kernel per tile entry");
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Fixed rule, from a sweep of every entry over the config-3 shapes on one MI355X: square-ish
-// problems take 256x256 when that alone fills the 256 CUs (4096^3: 1.05 PFLOP/s), else 128x128
-// with two workgroups per CU (2048x3072x8192: 860 TFLOP/s); skinny prefill problems (M < 512) take
-// the largest 4-stage tile that still gives >= 160 workgroups, the deep prefetch hiding the latency
-// of the streamed weights (256x16384x3072: 640 TFLOP/s), with 64x96 ahead of 128x64 where it fills
-// the CUs in one round. A K-32 stage variant (4 stages for 256x256) measured no faster than 2 stages
-// of K 64, so the plain entries keep K 64; the ping-pong entries are for sweeps.
-int choose_tile(int64_t M, int64_t N) {
+// Fixed rule, from sweeps of every entry (and K splits of 1-8) over the config-3 shapes on one
+// MI355X (graph replays, weights rotated past the MALL):
+//   * M >= 512: 256x256 when that alone fills the 256 CUs (4096^3: 1.05 PFLOP/s), else 128x128 with
+//     two workgroups per CU (2048x3072x8192: 117 us); K splits only lost here;
+//   * M < 512 with a workspace (gemm_f16_nt_ws): the pipelined 128x128 entry with K split so the
+//     tiles times the split come closest to 256 workgroups (256x5120x3072: 80 tiles x 3, 23.1 us;
+//     256x3072x8192: 48 x 5, 29 us; 256x16384x3072: 256 x 1, 40 us);
+//   * M < 512 without one: the largest 4-stage tile that still gives >= 160 workgroups (pipelined
+//     128x128, then 64x96 where it fills the CUs in one round, then 128x64, 64x64).
+// Measured and not in the list: whole-256-row tiles (256x64, 64x256, 256x32), 4 waves of 128x128 on
+// 256x256 tiles and of 64x128 / 128x64, K steps of 128, and the pipelined schedule on the 8-wave
+// 256x256 and the two-workgroup 128x128 entries: each equal or slower on every config-3 shape.
+int choose_tile(int64_t M, int64_t N, bool split_ok) {
   const char* ov = getenv("Q4_GEMM_CFG");
   if (ov && *ov) {
     const int i = atoi(ov);
@@ -499,10 +684,11 @@ int choose_tile(int64_t M, int64_t N) {
   }
   auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
   if (M >= 512) return tiles(0) >= 256 ? 0 : 4;
-  if (tiles(3) >= 160) return 3;
+  if (split_ok && N % 4 == 0) return 11;
+  if (tiles(11) >= 160) return 11;
   // 64x96 when it covers the CUs in one round (256x5120x3072: 160 workgroups of 128x64 -> 216 of 64x96,
   // 17% fewer bytes per CU, 27.6 -> 23.6 us)
-  if (tiles(10) >= 160 && tiles(10) <= 256) return 10;
+  if (tiles(12) >= 160 && tiles(12) <= 256) return 12;
   for (int i : {5, 6})
     if (tiles(i) >= 160) return i;
   return 6;
@@ -510,8 +696,39 @@ int choose_tile(int64_t M, int64_t N) {
 
 }  // namespace
 
+// K split of tile entry ti: n_split K ranges of nk_split K steps each (the last may be shorter, none
+// empty); {1, 0} for no split. Only the plain (not ping-pong) entries split, and only when N % 4 == 0
+// (the reduce kernel's four-column rows): M < 512 takes the split that brings the workgroups closest
+// to 256 without exceeding it, each range at least four K steps. Q4_GEMM_SPLIT forces a split count
+// for sweeps.
+struct GemmSplit {
+  int n_split, nk_split;
+};
+GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int ti) {
+  GemmSplit p{1, 0};
+  const TileCfg& t = kTiles[ti];
+  if (t.pp || N % 4 || M <= 1) return p;
+  const int nk = static_cast<int>(cdiv(K, t.bk));
+  const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  int want = M < 512 ? static_cast<int>(std::min<int64_t>(256 / tiles, nk / 4)) : 1;
+  const char* ov = getenv("Q4_GEMM_SPLIT");
+  if (ov && *ov) want = atoi(ov);
+  if (want <= 1 || nk < 2) return p;
+  const int nk_s = static_cast<int>(cdiv(nk, std::min(want, nk)));
+  const int S = static_cast<int>(cdiv(nk, nk_s));
+  if (S < 2) return p;
+  p.n_split = S;
+  p.nk_split = nk_s;
+  return p;
+}
+
+size_t gemm_split_bytes(int64_t M, int64_t N, int64_t K, int ti) {
+  const GemmSplit sp = gemm_split_plan(M, N, K, ti);
+  return sp.n_split > 1 ? static_cast<size_t>(sp.n_split) * M * N * sizeof(float) : 0;
+}
+
 int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                    int64_t ldb, int64_t ldc, int cfg, hipStream_t st) {
+                    int64_t ldb, int64_t ldc, int cfg, hipStream_t st, float* part = nullptr, size_t part_bytes = 0) {
   if (M == 1 && cfg < 0) {  // 2 rows per wave, 8 per workgroup; passes of up to 4096 k
     const unsigned grid = static_cast<unsigned>(cdiv(N, 8));
     if (K <= 1024)
@@ -524,7 +741,7 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
       hipLaunchKernelGGL((gemv_f16_kernel<2, 8>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
     return launch_status();
   }
-  const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N);
+  const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N, part != nullptr);
   const TileCfg& t = kTiles[ti];
   const int tiles_m = static_cast<int>(cdiv(M, t.bm)), tiles_n = static_cast<int>(cdiv(N, t.bn));
   const int ntiles = tiles_m * tiles_n;
@@ -533,10 +750,34 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
     Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kGemmFns[ti]),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   }
-  const int remap = (ntiles % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(kGemmFns[ti], dim3(ntiles, 1), dim3(64 * t.wgm * t.wgn), lds, st, A, B, C, (int)M, (int)N,
-                     (int)K, (int)lda, (int)ldb, (int)ldc, tiles_m, tiles_n, remap);
-  return launch_status();
+  GemmSplit sp{1, 0};
+  if (part) {
+    sp = gemm_split_plan(M, N, K, ti);
+    if (sp.n_split > 1 && (part_bytes < static_cast<size_t>(sp.n_split) * M * N * sizeof(float) || !aligned(part, 16)))
+      return Q4_ERR_WORKSPACE;
+  }
+  const int grid = ntiles * sp.n_split;
+  const int remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(kGemmFns[ti], dim3(grid, 1), dim3(64 * t.wgm * t.wgn), lds, st, A, B, C, (int)M, (int)N, (int)K,
+                     (int)lda, (int)ldb, (int)ldc, tiles_m, tiles_n, remap, sp.n_split, sp.nk_split, part);
+  if (int e = launch_status()) return e;
+  if (sp.n_split > 1) {
+    const unsigned blocks = static_cast<unsigned>(cdiv(M * N / 4, 256));
+    if (ldc % 4 == 0 && aligned(C, 8))
+      hipLaunchKernelGGL(gemm_split_reduce_kernel<true>, dim3(blocks), dim3(256), 0, st, part, C, (int)M, (int)N,
+                         (int)ldc, sp.n_split);
+    else
+      hipLaunchKernelGGL(gemm_split_reduce_kernel<false>, dim3(blocks), dim3(256), 0, st, part, C, (int)M, (int)N,
+                         (int)ldc, sp.n_split);
+    return launch_status();
+  }
+  return Q4_OK;
+}
+
+// Workspace bytes gemm_f16_nt_ws uses for this shape (0: no K split).
+size_t gemm_f16_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M == 1) return 0;
+  return gemm_split_bytes(M, N, K, choose_tile(M, N, true));
 }
 
 int gemm_f16_num_tiles() { return kNumTiles; }
@@ -544,8 +785,8 @@ int gemm_f16_num_tiles() { return kNumTiles; }
 int gemm_f16_tile_info(int i, int* out) {
   if (i < 0 || i >= kNumTiles) return Q4_ERR_RANGE;
   const TileCfg& t = kTiles[i];
-  const int v[7] = {t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.pp ? 1 : 0};
-  for (int j = 0; j < 7; ++j) out[j] = v[j];
+  const int v[8] = {t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.pp ? 1 : 0, t.sp ? 1 : 0};
+  for (int j = 0; j < 8; ++j) out[j] = v[j];
   return Q4_OK;
 }
 
@@ -567,6 +808,22 @@ extern "C" int gemm_f16_nt(const uint16_t* A, const uint16_t* B, uint16_t* C, in
                            int64_t lda, int64_t ldb, int64_t ldc, void* stream) {
   if (int st = gemm_args(A, B, C, M, N, K, lda, ldb, ldc)) return st;
   return q4::gemm_f16_launch(A, B, C, M, N, K, lda, ldb, ldc, -1, q4::as_stream(stream));
+}
+
+extern "C" int gemm_f16_nt_ws_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes) {
+  if (!bytes) return Q4_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return Q4_ERR_SHAPE;
+  *bytes = q4::gemm_f16_ws_bytes(M, N, K);
+  return Q4_OK;
+}
+
+extern "C" int gemm_f16_nt_ws(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
+                              int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (int st = gemm_args(A, B, C, M, N, K, lda, ldb, ldc)) return st;
+  if (M > 1 && !workspace && q4::gemm_f16_ws_bytes(M, N, K) > 0) return Q4_ERR_WORKSPACE;
+  return q4::gemm_f16_launch(A, B, C, M, N, K, lda, ldb, ldc, -1, q4::as_stream(stream),
+                             static_cast<float*>(workspace), workspace_bytes);
 }
 
 extern "C" int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,

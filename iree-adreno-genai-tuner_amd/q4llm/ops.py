@@ -210,6 +210,35 @@ def gemm_f16_nt(a, b, out=None):
     return out
 
 
+def gemm_f16_nt_ws_bytes(m, n, k) -> int:
+    b = C.c_size_t(0)
+    LIB.call("gemm_f16_nt_ws_bytes", m, n, k, C.byref(b))
+    return b.value
+
+
+def gemm_f16_nt_ws(a, b, out=None, workspace=None):
+    """gemm_f16_nt with a device workspace (uint8, >= gemm_f16_nt_ws_bytes): K split over several
+    workgroups per output tile where the tiles alone leave CUs idle, partials added in a fixed order.
+    A workspace is allocated when none is given."""
+    m, k = a.shape
+    n = b.shape[0]
+    _need(a, "A", torch.float16, (m, k), contiguous=False)
+    _need(b, "B", torch.float16, (n, k), contiguous=False)
+    _need(out, "C", torch.float16, (m, n), contiguous=False)
+    for t, nm in ((a, "A"), (b, "B"), (out, "C")):
+        if t is not None and t.stride(1) != 1:
+            raise ValueError(f"{nm}: rows must be contiguous (stride(1) == 1)")
+    _dev(a, b, out, workspace)
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.float16, device=a.device)
+    if workspace is None:
+        workspace = torch.empty(max(gemm_f16_nt_ws_bytes(m, n, k), 16), dtype=torch.uint8, device=a.device)
+    _need(workspace, "workspace", torch.uint8, None)
+    LIB.call("gemm_f16_nt_ws", ptr(a), ptr(b), ptr(out), m, n, k, a.stride(0), b.stride(0), out.stride(0),
+             ptr(workspace), workspace.numel(), stream_of(a.device))
+    return out
+
+
 def gemm_f16_nt_cfg(a, b, out, cfg=-1, split=0):
     """Benchmark hook: gemm_f16_nt with an explicit tile config index and split-K factor."""
     m, k = a.shape

@@ -123,6 +123,7 @@ def test_attn_prefill_chunk(dev, monkeypatch, Cn, start, L, nq, nkv, hd, path):
 
 GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 5120, 3072), (2048, 3072, 8192),
                (4096, 4096, 4096), (1, 3072, 3072)]
+GEMM_SHAPES_WS = GEMM_SHAPES[:4] + [(128, 5120, 3072), (1, 3072, 3072)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
@@ -167,6 +168,67 @@ def test_gemm_all_tiles_and_ragged_edges(dev):
             ops.gemm_f16_nt_cfg(A, B, c, cfg=cfg)
             err = (c.cpu().float() - ref).abs().max().item()
             assert err <= 1e-2 * ref.pow(2).mean().sqrt().item(), (M, N, K, cfg)
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES_WS)
+def test_gemm_ws_config3(dev, M, N, K):
+    """gemm_f16_nt_ws on the config-3 shapes (the 256-row ones split K and add the partials in a
+    second launch) against the host fp32 matmul, and against gemm_f16_nt."""
+    a, b = synth.gemm_problem(M, N, K, seed=1)
+    A, B = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    ws = torch.empty(max(ops.gemm_f16_nt_ws_bytes(M, N, K), 16), dtype=torch.uint8, device=dev)
+    c = nan_like((M, N), torch.float16, dev)
+    ops.gemm_f16_nt_ws(A, B, out=c, workspace=ws)
+    ref = torch.from_numpy(a).float() @ torch.from_numpy(b).float().T
+    rms = ref.pow(2).mean().sqrt().item()
+    err = (c.cpu().float() - ref).abs().max().item()
+    assert err <= 1e-2 * rms, (err, rms)
+    c2 = ops.gemm_f16_nt(A, B).cpu().float()
+    assert (c.cpu().float() - c2).abs().max().item() <= 1e-2 * rms
+
+
+def test_gemm_ws_forced_splits_every_plain_tile(dev, monkeypatch):
+    """Every plain tile entry with K split 2, 3 and 5 ways (ranges not a multiple of the stage count)
+    at a ragged shape, and twice in a row into the same workspace: host fp32 reference each time."""
+    from q4llm._lib import config_table
+    M, N, K = 200, 300, 136 + 64 * 9
+    a, b = synth.gemm_problem(M, N, K, seed=3)
+    A, B = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    ref = torch.from_numpy(a).float() @ torch.from_numpy(b).float().T
+    bar = 1e-2 * ref.pow(2).mean().sqrt().item()
+    ws = torch.empty(5 * M * N * 4, dtype=torch.uint8, device=dev)
+    for cfg, info in enumerate(config_table("gemm")):
+        if info[6]:
+            continue  # ping-pong entries do not split
+        monkeypatch.setenv("Q4_GEMM_CFG", str(cfg))
+        for S in (2, 3, 5):
+            monkeypatch.setenv("Q4_GEMM_SPLIT", str(S))
+            nk = -(-K // info[5])
+            s_eff = -(-nk // -(-nk // S))  # ranges of ceil(nk / S) steps, none empty (5 -> 4 at 12 steps)
+            assert ops.gemm_f16_nt_ws_bytes(M, N, K) == s_eff * M * N * 4
+            for _ in range(2):
+                c = nan_like((M, N), torch.float16, dev)
+                ops.gemm_f16_nt_ws(A, B, out=c, workspace=ws)
+                err = (c.cpu().float() - ref).abs().max().item()
+                assert err <= bar, (cfg, S, err)
+
+
+def test_gemm_ws_workspace_checks(dev):
+    from q4llm._lib import LIB
+    Q4_ERR_WORKSPACE = -5
+    M, N, K = 256, 3072, 8192
+    need = ops.gemm_f16_nt_ws_bytes(M, N, K)
+    assert need == 5 * M * N * 4
+    assert ops.gemm_f16_nt_ws_bytes(1024, 5120, 3072) == 0
+    A = torch.zeros(M, K, dtype=torch.float16, device=dev)
+    B = torch.zeros(N, K, dtype=torch.float16, device=dev)
+    C = torch.empty(M, N, dtype=torch.float16, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    f = LIB.raw("gemm_f16_nt_ws")
+    assert f(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, K, K, N, None, 0, None) == Q4_ERR_WORKSPACE
+    assert f(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, K, K, N, ws.data_ptr(), need - 16,
+             None) == Q4_ERR_WORKSPACE
+    torch.cuda.synchronize()
 
 
 # ------------------------------------------------------------------------------------------------

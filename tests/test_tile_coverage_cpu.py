@@ -236,56 +236,96 @@ def tile_of(bid, tiles_m, tiles_n, remap):
     return first_m + in_group % gsize, in_group // gsize
 
 
-def replay_gemm(cfg, M, N, K):
-    bm, bn, wm, wn, nst, bk, pp = cfg
+def gemm_split(cfg, M, N, K, force=None):
+    """K split of a tile entry (csrc/gemm_f16.hip: gemm_split_plan): (n_split, nk_split)."""
+    bm, bn, wm, wn, nst, bk, pp, sp = cfg
+    if pp or N % 4 or M <= 1:
+        return 1, 0
+    nk = cdiv(K, bk)
+    tiles = cdiv(M, bm) * cdiv(N, bn)
+    want = min(256 // tiles, nk // 4) if M < 512 else 1
+    if force is not None:
+        want = force
+    if want <= 1 or nk < 2:
+        return 1, 0
+    nk_s = cdiv(nk, min(want, nk))
+    S = cdiv(nk, nk_s)
+    return (S, nk_s) if S >= 2 else (1, 0)
+
+
+def replay_gemm(cfg, M, N, K, force_split=None):
+    """gemm_f16_nt_kernel / gemm_f16_nt_pp_kernel: workgroup -> (K range, tile) mapping, the direct
+    loads of one stage (lane offsets, row blocks, LDS slots), operand reads and epilogue stores."""
+    bm, bn, wm, wn, nst, bk, pp, sp = cfg
     waves = wm * wn
     row_b = bk * 2
     rows_per_inst = 1024 // row_b
     kcpr = bk // 8
     kai = cdiv(bm // rows_per_inst, waves)
     kbi = cdiv(bn // rows_per_inst, waves)
+    rows_per_j = waves * rows_per_inst
     tiles_m, tiles_n = cdiv(M, bm), cdiv(N, bn)
     ntiles = tiles_m * tiles_n
-    remap = 1 if ntiles % 8 == 0 else 0
-    seen = np.zeros((tiles_m, tiles_n), np.int32)
-    for bid in range(ntiles):
-        tm, tn = tile_of(bid, tiles_m, tiles_n, remap)
-        seen[tm, tn] += 1
-    assert (seen == 1).all(), "tile order is not a permutation"
+    nk = cdiv(K, bk)
+    S, nk_s = gemm_split(cfg, M, N, K, force_split)
+    grid = ntiles * S
+    remap = 1 if grid % 8 == 0 else 0
+    seen = np.zeros((S, tiles_m, tiles_n), np.int32)
+    for g in range(grid):
+        gg = (g % 8) * (grid // 8) + g // 8 if remap else g
+        ksp = gg // ntiles
+        tm, tn = tile_of(gg - ksp * ntiles, tiles_m, tiles_n, 0)
+        seen[ksp, tm, tn] += 1
+    assert (seen == 1).all(), "workgroup order is not a permutation of (K range, tile)"
+    ksteps = np.zeros(nk, np.int32)
+    for ksp in range(S):
+        kt0 = ksp * nk_s if S > 1 else 0
+        n = min(nk_s, nk - kt0) if S > 1 else nk
+        assert n >= 1, "empty K range"
+        ksteps[kt0:kt0 + n] += 1
+    assert (ksteps == 1).all(), "K steps reduced other than once"
     lane = np.arange(64)
     lda = ldb = K
     abytes, bbytes = (M - 1) * lda * 2 + K * 2, (N - 1) * ldb * 2 + K * 2
-    # one stage of one tile (m0 = n0 = 0 covers the in-range rows; a ragged last tile below)
+    # one stage of the first and of the last (ragged) tile, at the first and the last K step
     for (m0, n0) in ((0, 0), ((tiles_m - 1) * bm, (tiles_n - 1) * bn)):
+        full = m0 + bm <= M and n0 + bn <= N
         for nrows, base, nbytes, ld, ni, limit in ((bm, m0, abytes, lda, kai, M), (bn, n0, bbytes, ldb, kbi, N)):
-            filled = np.zeros((nrows, kcpr), np.int32)
-            for k0 in range(0, K, bk):
-                filled[:] = 0
+            for k0 in (0, (nk - 1) * bk):
+                filled = np.zeros((nrows, kcpr), np.int32)
+                fast = full and k0 + bk <= K
                 for wave in range(waves):
+                    r0 = wave * rows_per_inst + lane // kcpr
+                    chunk = (lane % kcpr) ^ swz(bk, r0)
+                    lane_off = (base + r0) * ld * 2 + chunk * 16
+                    left = limit - base - r0
                     for j in range(ni):
                         blk = wave + j * waves
-                        r = blk * rows_per_inst + lane // kcpr
+                        r = r0 + j * rows_per_j
                         real = blk < nrows // rows_per_inst
-                        if not pp:
-                            assert real or j >= 1 or blk < nrows // rows_per_inst
-                        elif not real:
+                        if pp and not real:
                             pytest.fail("ping-pong loads must divide evenly")
                         if not real:
                             continue  # spare instructions land in the junk area
-                        chunk = (lane % kcpr) ^ swz(bk, r)
+                        # the chunk formula of row r gives the lane's chunk for every j
+                        assert (chunk == ((lane % kcpr) ^ swz(bk, r))).all()
                         for ln in range(64):
-                            slot = ln % kcpr
                             g_row, g_k = base + r[ln], k0 + 8 * chunk[ln]
                             in_range = g_row < limit and g_k < K
-                            off = (g_row * ld * 2 + chunk[ln] * 16 + k0 * 2) if in_range else OOB
+                            if fast:
+                                off = lane_off[ln] + k0 * 2 + j * rows_per_j * ld * 2
+                                assert in_range
+                            else:
+                                ok = g_k < K and j * rows_per_j < left[ln]
+                                assert ok == in_range
+                                off = lane_off[ln] + j * rows_per_j * ld * 2 + k0 * 2 if ok else OOB
                             assert off < 2 ** 31 or off == OOB
                             if in_range:
-                                assert off < nbytes
-                            filled[r[ln], slot] += 1
+                                assert off == g_row * ld * 2 + g_k * 2 and off < nbytes
+                            filled[r[ln], ln % kcpr] += 1
                             # the reader of (row, chunk c) looks at slot c ^ swz(row): it holds chunk c
-                            assert (slot ^ swz(bk, r[ln])) == chunk[ln]
+                            assert ((ln % kcpr) ^ swz(bk, r[ln])) == chunk[ln]
                 assert (filled == 1).all(), "LDS stage slots filled other than once"
-                break  # the pattern is the same for every k step; K raggedness is the g_k < K test
     # operand reads: lane supplies row lane % 32 and chunk 2 kk + lane / 32 of each 16-k step
     ks = np.zeros(bk // 8, np.int32)
     for kk in range(bk // 16):
@@ -309,8 +349,21 @@ def replay_gemm(cfg, M, N, K):
 @pytest.mark.parametrize("idx", range(len(config_table("gemm"))))
 def test_gemm_entries_cover_once(idx):
     cfg = config_table("gemm")[idx]
-    for (M, N, K) in ((300, 520, 200), (cfg[0] * 2, cfg[1] * 4, 512)):
+    for (M, N, K) in ((300, 520, 200), (cfg[0] * 2, cfg[1] * 4, 512), (256, 3072, 8192)):
         replay_gemm(cfg, M, N, K)
+    if not cfg[6]:  # K splits (plain entries): forced counts, ragged K, and the automatic rule
+        for force in (2, 3, 5):
+            replay_gemm(cfg, 300, 520, 200 + 64 * 9, force)
+        replay_gemm(cfg, 256, 5120, 3072)
+
+
+def test_gemm_split_rule_fills_the_cus():
+    """The automatic K split of the 256-row config-3 shapes on the pipelined 128x128 entry."""
+    cfg = next(c for c in config_table("gemm") if c[:6] == (128, 128, 2, 2, 4, 64) and c[7])
+    assert gemm_split(cfg, 256, 5120, 3072) == (3, 16)   # 80 tiles x 3
+    assert gemm_split(cfg, 256, 3072, 8192) == (5, 26)   # 48 tiles x 5 (last range 24 steps)
+    assert gemm_split(cfg, 256, 16384, 3072) == (1, 0)   # 256 tiles fill the CUs
+    assert gemm_split(cfg, 1024, 5120, 3072) == (1, 0)   # no split from 512 rows on
 
 
 # ------------------------------------------------------------------------------------------------
