@@ -278,7 +278,29 @@ GEMM_SHAPES = [(256, 5120, 3072), (256, 16384, 3072), (256, 3072, 8192), (1024, 
                (4096, 4096, 4096), (1, 3072, 3072)]
 
 
-def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
+def vendor_gemm_us(A, B, Bs, reps=5):
+    """Median / min us per launch of torch.matmul(A, B^T) (hipBLASLt on this image) over the same rotated
+    B copies: plain stream launches bracketed by HIP events (no graph capture: library calls stay out
+    of graphs here), the rotation run once untimed first."""
+    import statistics
+    import torch
+    n = max(16, 2 * len(Bs))
+    for b in Bs:
+        torch.matmul(A, b.t())
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            torch.matmul(A, Bs[i % len(Bs)].t())
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / n)
+    return round(statistics.median(ts), 3), round(min(ts), 3)
+
+
+def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5, vendor=False):
     """Config 3 through gemm_f16_nt_ws (the 256-row shapes split K over a workspace allocated once per
     shape, outside the timed region). Parity against the host fp32 matmul of the same fp16 inputs
     (gemm/shapes.py:62), whose wall time on this host's cores is the leg's CPU figure; error is
@@ -323,6 +345,11 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5):
                                "cpu_cores": cores, "cpu_reps": cpu_n}
         log(f"gemm {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}) {tf:.1f} TFLOP/s "
             f"({tf / attain:.1%} of attainable {attain:.0f}); host fp32 {cpu_ms:.2f} ms; err/rms {err:.2e}")
+        if vendor and M > 1:
+            v_med, v_min = vendor_gemm_us(A, B0, Bs)
+            out[f"{M}x{N}x{K}"].update({"hipblaslt_us": v_med, "hipblaslt_us_min": v_min,
+                                        "hipblaslt_TFLOP/s": round(flops / v_med / 1e6, 1)})
+            log(f"  torch.matmul (hipBLASLt) {v_med:.2f} us (min {v_min:.2f}) {flops / v_med / 1e6:.1f} TFLOP/s")
         del A, B0, Bs, C, ws
         torch.cuda.empty_cache()
     return out
@@ -501,6 +528,8 @@ def main():
     ap.add_argument("--skip-e2e", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true", help="leave out every CPU-baseline figure")
     ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="also time torch.matmul (hipBLASLt) on the GEMM shapes, for comparison")
     ap.add_argument("--skip-attn", action="store_true")
     ap.add_argument("--skip-gemv", action="store_true",
                     help="leave out the GEMV and probe legs (profiling the other legs; the line then has no value)")
@@ -534,7 +563,8 @@ def main():
                "unit": "GB/s", "note": "--skip-gemv: profiling run of the other legs"}
         if not a.skip_gemm:
             out["gemm_f16"] = bench_gemm(dev, GEMM_SHAPES if a.gemm_shapes is None else
-                                         [tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes])
+                                         [tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes],
+                                         vendor=a.vendor_gemm)
         if not a.skip_attn:
             out["attn_decode"] = bench_attn(dev)
         if not a.skip_e2e:
@@ -605,7 +635,7 @@ def main():
     if not a.skip_gemm:
         shapes = ([tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes] if a.gemm_shapes is not None
                   else GEMM_SHAPES)
-        out["gemm_f16"] = bench_gemm(dev, shapes)
+        out["gemm_f16"] = bench_gemm(dev, shapes, vendor=a.vendor_gemm)
     if not a.skip_attn:
         out["attn_decode"] = bench_attn(dev)
     if not a.skip_e2e:

@@ -674,8 +674,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //   * M < 512 without one: the largest 4-stage tile that still gives >= 160 workgroups (pipelined
 //     128x128, then 64x96 where it fills the CUs in one round, then 128x64, 64x64).
 // Measured and not in the list: whole-256-row tiles (256x64, 64x256, 256x32), 4 waves of 128x128 on
-// 256x256 tiles and of 64x128 / 128x64, K steps of 128, and the pipelined schedule on the 8-wave
-// 256x256 and the two-workgroup 128x128 entries: each equal or slower on every config-3 shape.
+// 256x256 tiles (2 stages of K 64, or 4-5 stages of K 32) and of 64x128 / 128x64, K steps of 128,
+// and the pipelined schedule on the 8-wave 256x256 and the two-workgroup 128x128 entries: each equal
+// or slower on every config-3 shape.
 int choose_tile(int64_t M, int64_t N, bool split_ok) {
   const char* ov = getenv("Q4_GEMM_CFG");
   if (ov && *ov) {
