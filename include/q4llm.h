@@ -364,8 +364,7 @@ int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
  *   q4_gemv_config_info:    lanes per row, chunks per lane, rows per lane, waves, x words, grid-stride
  *   q4_gemv_mx_config_info: row blocks per workgroup, waves per row block, tiles per wave, used rows
  *                           per 16-row block, grid-stride (q4_gemv_mx_num_configs entries)
- *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, ping-pong, pipelined
- *                           substeps (8 ints)
+ *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, pipelined substeps
  *   q4_linear_ws_config_info: BM, BN, wave rows, wave columns, stages, k-split */
 int q4_gemv_config_info(int cfg, int* info);
 int q4_gemv_mx_num_configs(void);

@@ -400,177 +400,6 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
   }
 }
 
-// Ping-pong variant of the kernel above for 8 waves (WM = 2, WN = 4) and an NST-stage ring.
-//
-// In the kernel above both waves of a SIMD run the same phase at the same time: both read their
-// operands from LDS, then both issue MFMAs, so the matrix core idles during the reads (with no
-// global loads and no barriers at all, 4096^3 still ran at only 56% of the MFMA peak). Here the
-// two wave rows form two groups (waves 0-3 and 4-7, one of each on every SIMD) that alternate
-// between a memory phase (LDS operand reads of one K step, and its share of the direct loads of a
-// later stage) and a compute phase (the step's MFMAs from registers); workgroup barriers separate
-// the phases, and group 1 starts one barrier late, so in every interval one wave of each SIMD feeds
-// the matrix core while the other reads LDS.
-//
-// Slots (intervals between barriers) s = 0, 1, ...: group 0 runs memory(k) in slot 2k and
-// compute(k) in slot 2k + 1; group 1 runs memory(k) in slot 2k + 1 and compute(k) in slot 2k + 2.
-// Stage k (LDS buffer k % NST) is read in slots 2k and 2k + 1, so it is free from slot 2k + 2 on,
-// where both groups issue their loads of stage k + NST (group 0 in memory(k + 1), group 1 in
-// compute(k)). Stage s must have landed by the end of slot 2s - 1 (group 0: end of compute(s - 1);
-// group 1: end of memory(s - 1)); each wave then has issued its loads up to stage s + NST - 2, so
-// it waits with vmcnt = (NST - 2) loads-per-stage, and the barrier publishes the stage. Stages past
-// the end are issued too, as out-of-range loads (zeros into a free buffer nobody reads), which keeps
-// that count exact. Every wave ends its memory phase with its LDS reads complete (lgkmcnt 0), so no
-// read is outstanding when a buffer is refilled. Both groups execute 2 nk + 2 barriers: group 1
-// one extra at the start, group 0 one extra at the end.
-template <int BM, int BN, int NST, int BK>
-__global__ __launch_bounds__(512) void gemm_f16_nt_pp_kernel(const uint16_t* __restrict__ A,
-                                                              const uint16_t* __restrict__ B, uint16_t* __restrict__ Cm,
-                                                              int M, int N, int K, int lda, int ldb, int ldc,
-                                                              int tiles_m, int tiles_n, int xcd_remap, int, int,
-                                                              float*) {  // no K split
-  constexpr int WM = 2, WN = 4;
-  using G = GemmCfg<BM, BN, WM, WN, NST, BK>;
-  static_assert(G::kLPW * (NST - 1) < 64, "vmcnt holds at most 63 loads");
-  static_assert(G::kAI * G::kRowsPerInst * G::kWaves == BM && G::kBI * G::kRowsPerInst * G::kWaves == BN,
-                "the ping-pong loads divide evenly over the waves");
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-
-  int bid = blockIdx.x;
-  const int ntiles = tiles_m * tiles_n;
-  if (xcd_remap) bid = (bid % 8) * (ntiles / 8) + bid / 8;
-  constexpr int kGroupM = 4;
-  const int group = bid / (kGroupM * tiles_n);
-  const int first_m = group * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
-  const int in_group = bid - group * (kGroupM * tiles_n);
-  const int tm = first_m + in_group % gsize, tn = in_group / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, static_cast<uint32_t>(M - 1) * lda * 2u + K * 2u);
-  const __amdgpu_buffer_rsrc_t br = make_rsrc(B, static_cast<uint32_t>(N - 1) * ldb * 2u + K * 2u);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / WN, wn = wave % WN;  // wm is the ping-pong group
-
-  constexpr int kCpr = BK / 8;
-  uint32_t aoff[G::kAI], boff[G::kBI];
-  int achunk[G::kAI], bchunk[G::kBI];
-#pragma unroll
-  for (int j = 0; j < G::kAI; ++j) {
-    const int r = (wave + j * G::kWaves) * G::kRowsPerInst + lane / kCpr;
-    achunk[j] = (lane % kCpr) ^ swz<BK>(r);
-    aoff[j] = m0 + r < M ? static_cast<uint32_t>(m0 + r) * lda * 2u + achunk[j] * 16u : kOOB;
-  }
-#pragma unroll
-  for (int j = 0; j < G::kBI; ++j) {
-    const int r = (wave + j * G::kWaves) * G::kRowsPerInst + lane / kCpr;
-    bchunk[j] = (lane % kCpr) ^ swz<BK>(r);
-    boff[j] = n0 + r < N ? static_cast<uint32_t>(n0 + r) * ldb * 2u + bchunk[j] * 16u : kOOB;
-  }
-  auto issue = [&](int kt) {
-    const int k0 = kt * BK;
-    unsigned char* sa = lds + (kt % NST) * G::kStage;
-    unsigned char* sb = sa + BM * G::kRow;
-#pragma unroll
-    for (int j = 0; j < G::kAI; ++j)
-      load_lds16(ar, sa + (wave + j * G::kWaves) * 1024,
-                 k0 + 8 * achunk[j] < K && aoff[j] != kOOB ? aoff[j] + k0 * 2u : kOOB);
-#pragma unroll
-    for (int j = 0; j < G::kBI; ++j)
-      load_lds16(br, sb + (wave + j * G::kWaves) * 1024,
-                 k0 + 8 * bchunk[j] < K && boff[j] != kOOB ? boff[j] + k0 * 2u : kOOB);
-  };
-
-  float16v acc[G::TM][G::TN];
-#pragma unroll
-  for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < G::TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-  const int arow = wm * G::WTM + (lane & 31);
-  const int brow = wn * G::WTN + (lane & 31);
-  half8 af[BK / 16][G::TM], bf[BK / 16][G::TN];
-  auto read_ops = [&](int kt) {
-    const unsigned char* sa = lds + (kt % NST) * G::kStage;
-    const unsigned char* sb = sa + BM * G::kRow;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int sw = ((2 * kk + (lane >> 5)) ^ swz<BK>(lane & 31)) << 4;
-#pragma unroll
-      for (int i = 0; i < G::TM; ++i) af[kk][i] = *reinterpret_cast<const half8*>(sa + (arow + 32 * i) * G::kRow + sw);
-#pragma unroll
-      for (int j = 0; j < G::TN; ++j) bf[kk][j] = *reinterpret_cast<const half8*>(sb + (brow + 32 * j) * G::kRow + sw);
-    }
-  };
-  auto mfmas = [&]() {
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk)
-#pragma unroll
-      for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < G::TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
-  };
-  // Phase boundary: nothing moves across it (the MFMAs are pure register operations, which the
-  // compiler would otherwise be free to move past a barrier).
-  auto bar = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  auto wait_lds = [&]() { __builtin_amdgcn_s_waitcnt(0xC07F); };  // lgkmcnt(0), vmcnt and expcnt unconstrained
-
-  const int nk = (K + BK - 1) / BK;
-#pragma unroll
-  for (int st = 0; st < NST; ++st) issue(st);
-  wait_vmcnt<(NST - 1) * G::kLPW>();  // stage 0 landed
-  bar();
-  if (wm == 0) {
-    for (int k = 0; k < nk; ++k) {
-      // memory(k), slot 2k: loads of stage k - 1 + NST (stage k - 1 was read in slots 2k - 2, 2k - 1),
-      // reads of stage k
-      if (k >= 1) issue(k - 1 + NST);
-      read_ops(k);
-      wait_lds();
-      bar();
-      // compute(k), slot 2k + 1; then this wave's loads of stage k + 1 have landed
-      mfmas();
-      wait_vmcnt<(NST - 2) * G::kLPW>();
-      bar();
-    }
-    bar();  // pairs with group 1's last barrier
-  } else {
-    bar();  // start one slot behind group 0
-    for (int k = 0; k < nk; ++k) {
-      // memory(k), slot 2k + 1; then this wave's loads of stage k + 1 have landed
-      read_ops(k);
-      wait_lds();
-      wait_vmcnt<(NST - 2) * G::kLPW>();
-      bar();
-      // compute(k), slot 2k + 2: stage k has been read by both groups, its buffer takes stage k + NST
-      issue(k + NST);
-      mfmas();
-      bar();
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < G::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < G::TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-        const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
-        if (row < M && col < N) Cm[static_cast<int64_t>(row) * ldc + col] = float_to_half_bits(acc[i][j][e]);
-      }
-}
-
 // fp16 GEMV for M == 1 (the gemv_nt shape): each wave owns kRows rows; its 64 lanes cover K in
 // 16-byte chunks (8 k), kKc chunks per lane per pass, so one pass spans 512 * kKc k. Every load of a
 // pass (x and the rows) is issued before any use; v_dot2_f32_f16 with fp32 accumulation, then a
@@ -615,24 +444,16 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
 
 struct TileCfg {
   int bm, bn, wgm, wgn, nst, bk;
-  bool pp = false;  // ping-pong schedule (gemm_f16_nt_pp_kernel: 8 waves as 2 x 4)
   bool sp = false;  // software-pipelined substeps (gemm_f16_nt_kernel<..., true>)
 };
 // Explicit CDNA4 tile list (index stable for gemm_f16_nt_cfg / Q4_GEMM_CFG).
 constexpr TileCfg kTiles[] = {
-    {256, 256, 2, 4, 2, 64},  // 0: 8 waves of 128x64, 2 stages of K 64 (128 KB LDS)
-    {256, 128, 4, 2, 3, 64},  // 1: 8 waves of 64x64, 3 stages (144 KB)
-    {128, 256, 2, 4, 3, 64},  // 2: 8 waves of 64x64, 3 stages (144 KB)
-    {128, 128, 2, 2, 4, 64},  // 3: 4 waves of 64x64, 4 stages (128 KB)
-    {128, 128, 2, 2, 2, 64},  // 4: 4 waves of 64x64, 2 stages (64 KB, two workgroups per CU)
-    {128, 64, 2, 2, 4, 64},   // 5: 4 waves of 64x32, 4 stages (96 KB)
-    {64, 64, 2, 2, 4, 64},    // 6: 4 waves of 32x32, 4 stages (64 KB)
-    {256, 256, 2, 4, 2, 64, true},  // 7: entry 0 with the ping-pong schedule
-    {256, 256, 2, 4, 4, 32, true},  // 8: ping-pong, 4 stages of K 32 (128 KB)
-    {256, 128, 2, 4, 3, 64, true},  // 9: 8 waves of 128x32, ping-pong, 3 stages (144 KB)
-    {64, 96, 2, 3, 4, 64},          // 10: 6 waves of 32x32, 4 stages (81 KB): M = 256, N = 5120 on 216 CUs
-    {128, 128, 2, 2, 4, 64, false, true},  // 11: entry 3 with software-pipelined substeps
-    {64, 96, 2, 3, 4, 64, false, true},    // 12: entry 10 with software-pipelined substeps
+    {256, 256, 2, 4, 2, 64},        // 0: 8 waves of 128x64, 2 stages of K 64 (128 KB LDS)
+    {128, 128, 2, 2, 2, 64},        // 1: 4 waves of 64x64, 2 stages (64 KB, two workgroups per CU)
+    {128, 128, 2, 2, 4, 64, true},  // 2: 4 waves of 64x64, 4 stages (128 KB), pipelined substeps
+    {64, 96, 2, 3, 4, 64, true},    // 3: 6 waves of 32x32, 4 stages (81 KB), pipelined: M = 256, N = 5120 on 216 CUs
+    {128, 64, 2, 2, 4, 64},         // 4: 4 waves of 64x32, 4 stages (96 KB)
+    {64, 64, 2, 2, 4, 64},          // 5: 4 waves of 32x32, 4 stages (64 KB)
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -642,24 +463,16 @@ using GemmFn = void (*)(const uint16_t*, const uint16_t*, uint16_t*, int, int, i
 template <int I>
 constexpr GemmFn gemm_fn() {
   constexpr TileCfg t = kTiles[I];
-  if constexpr (t.pp) {
-    static_assert(t.wgm == 2 && t.wgn == 4, "ping-pong entries are 2 x 4 waves");
-    return gemm_f16_nt_pp_kernel<t.bm, t.bn, t.nst, t.bk>;
-  } else {
-    return gemm_f16_nt_kernel<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.sp>;
-  }
+  return gemm_f16_nt_kernel<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.sp>;
 }
 template <int I>
 constexpr size_t gemm_lds() {
   constexpr TileCfg t = kTiles[I];
   return GemmCfg<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>::kLds;
 }
-constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>(),
-                               gemm_fn<5>(), gemm_fn<6>(), gemm_fn<7>(), gemm_fn<8>(), gemm_fn<9>(),
-                               gemm_fn<10>(), gemm_fn<11>(), gemm_fn<12>()};
+constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>(), gemm_fn<5>()};
 constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(), gemm_lds<4>(),
-                               gemm_lds<5>(), gemm_lds<6>(), gemm_lds<7>(), gemm_lds<8>(), gemm_lds<9>(),
-                               gemm_lds<10>(), gemm_lds<11>(), gemm_lds<12>()};
+                               gemm_lds<5>()};
 static_assert(sizeof(kGemmFns) / sizeof(kGemmFns[0]) == kNumTiles, "one kernel per tile entry");
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -674,9 +487,11 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //   * M < 512 without one: the largest 4-stage tile that still gives >= 160 workgroups (pipelined
 //     128x128, then 64x96 where it fills the CUs in one round, then 128x64, 64x64).
 // Measured and not in the list: whole-256-row tiles (256x64, 64x256, 256x32), 4 waves of 128x128 on
-// 256x256 tiles (2 stages of K 64, or 4-5 stages of K 32) and of 64x128 / 128x64, K steps of 128,
-// and the pipelined schedule on the 8-wave 256x256 and the two-workgroup 128x128 entries: each equal
-// or slower on every config-3 shape.
+// 256x256 tiles (2 stages of K 64, or 4-5 stages of K 32) and of 64x128 / 128x64, 8 waves on 256x128
+// and 128x256, K steps of 128, the plain schedule on the 4-stage 128x128 and 64x96 tiles (the
+// pipelined ones replace them), the pipelined schedule on the 8-wave 256x256 and the two-workgroup
+// 128x128 entries, and a ping-pong schedule of two 4-wave groups on 256x256: each equal or slower on
+// every config-3 shape.
 int choose_tile(int64_t M, int64_t N, bool split_ok) {
   const char* ov = getenv("Q4_GEMM_CFG");
   if (ov && *ov) {
@@ -684,31 +499,30 @@ int choose_tile(int64_t M, int64_t N, bool split_ok) {
     if (i >= 0 && i < kNumTiles) return i;
   }
   auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
-  if (M >= 512) return tiles(0) >= 256 ? 0 : 4;
-  if (split_ok && N % 4 == 0) return 11;
-  if (tiles(11) >= 160) return 11;
+  if (M >= 512) return tiles(0) >= 256 ? 0 : 1;
+  if (split_ok && N % 4 == 0) return 2;
+  if (tiles(2) >= 160) return 2;
   // 64x96 when it covers the CUs in one round (256x5120x3072: 160 workgroups of 128x64 -> 216 of 64x96,
   // 17% fewer bytes per CU, 27.6 -> 23.6 us)
-  if (tiles(12) >= 160 && tiles(12) <= 256) return 12;
-  for (int i : {5, 6})
+  if (tiles(3) >= 160 && tiles(3) <= 256) return 3;
+  for (int i : {4, 5})
     if (tiles(i) >= 160) return i;
-  return 6;
+  return 5;
 }
 
 }  // namespace
 
 // K split of tile entry ti: n_split K ranges of nk_split K steps each (the last may be shorter, none
-// empty); {1, 0} for no split. Only the plain (not ping-pong) entries split, and only when N % 4 == 0
-// (the reduce kernel's four-column rows): M < 512 takes the split that brings the workgroups closest
-// to 256 without exceeding it, each range at least four K steps. Q4_GEMM_SPLIT forces a split count
-// for sweeps.
+// empty); {1, 0} for no split. Only when N % 4 == 0 (the reduce kernel's four-column rows): M < 512
+// takes the split that brings the workgroups closest to 256 without exceeding it, each range at least
+// four K steps. Q4_GEMM_SPLIT forces a split count for sweeps.
 struct GemmSplit {
   int n_split, nk_split;
 };
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int ti) {
   GemmSplit p{1, 0};
   const TileCfg& t = kTiles[ti];
-  if (t.pp || N % 4 || M <= 1) return p;
+  if (N % 4 || M <= 1) return p;
   const int nk = static_cast<int>(cdiv(K, t.bk));
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   int want = M < 512 ? static_cast<int>(std::min<int64_t>(256 / tiles, nk / 4)) : 1;
@@ -786,8 +600,8 @@ int gemm_f16_num_tiles() { return kNumTiles; }
 int gemm_f16_tile_info(int i, int* out) {
   if (i < 0 || i >= kNumTiles) return Q4_ERR_RANGE;
   const TileCfg& t = kTiles[i];
-  const int v[8] = {t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.pp ? 1 : 0, t.sp ? 1 : 0};
-  for (int j = 0; j < 8; ++j) out[j] = v[j];
+  const int v[7] = {t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk, t.sp ? 1 : 0};
+  for (int j = 0; j < 7; ++j) out[j] = v[j];
   return Q4_OK;
 }
 

@@ -640,26 +640,17 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float4* __rest
 struct LinWsTile {
   int bm, bn, wm, wn, nst, ks;
 };
-// Explicit tile list (index stable for Q4_LINEAR_CFG sweeps).
+// Explicit tile list (index stable for Q4_LINEAR_CFG sweeps): the entries the rules below pick. Swept
+// and removed (slower on every 3B prefill shape at M = 128, 256 and 1024): 4-wave 64x64, 32x64 and
+// 64x128 wave tiles on 128x128, 64x128, 128x64 and 64x256, 32x128 wave tiles (4 or 8 waves on 64x256,
+// 128x128, 128x256, 64x512), 64x64 waves on 128x256, k-split 2-wave and 64x64 / 128x64 / 32x96 /
+// 32x128 / 32x160 variants.
 constexpr LinWsTile kLinWsTiles[] = {
     {64, 64, 2, 2, 4, 1},    // 0: 4 waves of 32x32, 4 stages (77 KB)
     {32, 64, 1, 2, 4, 2},    // 1: 4 waves: 2 tiles of 32x32, each k-split over 2 waves (52 KB)
-    {64, 64, 2, 2, 4, 2},    // 2: 8 waves: 4 tiles of 32x32, k-split over 2
-    {128, 64, 2, 2, 4, 2},   // 3: 8 waves: 4 tiles of 64x32, k-split over 2
-    {32, 32, 1, 1, 4, 2},    // 4: 2 waves: one 32x32 tile, k-split over 2
-    {128, 128, 2, 2, 4, 1},  // 5: 4 waves of 64x64 (152 KB)
-    {64, 128, 2, 2, 4, 1},   // 6: 4 waves of 32x64
-    {64, 128, 2, 2, 4, 2},   // 7: 8 waves: 4 tiles of 32x64, k-split over 2
-    {32, 128, 1, 2, 4, 2},   // 8: 4 waves: 2 tiles of 32x64, k-split over 2
-    {128, 64, 2, 2, 4, 1},   // 9: 4 waves of 64x32
-    // one workgroup per CU at M = 256 for N = 5120, 16384 and 3072 (x re-read over fewer column tiles)
-    {32, 160, 1, 5, 4, 1},   // 10: 5 waves of 32x32
-    {32, 160, 1, 5, 4, 2},   // 11: 10 waves, k-split over 2
-    {64, 256, 2, 4, 4, 1},   // 12: 8 waves of 32x64
-    {64, 256, 1, 4, 4, 1},   // 13: 4 waves of 64x64
-    {32, 96, 1, 3, 4, 2},    // 14: 6 waves: 3 tiles of 32x32, k-split over 2
-    {32, 96, 1, 3, 4, 1},    // 15: 3 waves of 32x32
+    {64, 256, 2, 4, 4, 1},   // 2: 8 waves of 32x64: one workgroup per CU for 256-row chunks, and the K split
 };
+constexpr int kSplitTile = 2;  // the K-split tile (linear_split_plan) and the SwiGLU-epilogue tile
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
                          int, int, int, int, int, int, float*);
 template <int I>
@@ -672,14 +663,8 @@ constexpr size_t lin_ws_lds() {
   constexpr LinWsTile t = kLinWsTiles[I];
   return LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
 }
-constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(),  lin_ws_fn<1>(),  lin_ws_fn<2>(),  lin_ws_fn<3>(),
-                                 lin_ws_fn<4>(),  lin_ws_fn<5>(),  lin_ws_fn<6>(),  lin_ws_fn<7>(),
-                                 lin_ws_fn<8>(),  lin_ws_fn<9>(),  lin_ws_fn<10>(), lin_ws_fn<11>(),
-                                 lin_ws_fn<12>(), lin_ws_fn<13>(), lin_ws_fn<14>(), lin_ws_fn<15>()};
-constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(),  lin_ws_lds<1>(),  lin_ws_lds<2>(),  lin_ws_lds<3>(),
-                                lin_ws_lds<4>(),  lin_ws_lds<5>(),  lin_ws_lds<6>(),  lin_ws_lds<7>(),
-                                lin_ws_lds<8>(),  lin_ws_lds<9>(),  lin_ws_lds<10>(), lin_ws_lds<11>(),
-                                lin_ws_lds<12>(), lin_ws_lds<13>(), lin_ws_lds<14>(), lin_ws_lds<15>()};
+constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>()};
+constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>()};
 static_assert(sizeof(kLinWsFns) / sizeof(kLinWsFns[0]) == sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]),
               "one kernel per tile entry");
 constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
@@ -733,7 +718,7 @@ int planes_args(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t
 }
 }  // namespace
 
-// K split of the 64x256 tile (entry 12) for a chunk of M <= 256 rows whose tiles alone would leave
+// K split of the 64x256 tile (kSplitTile) for a chunk of M <= 256 rows whose tiles alone would leave
 // CUs idle: about 256 / tiles splits, each a whole number of groups (64-k stages, at least one group).
 LinearSplit linear_split_plan(int64_t M, int64_t N, int64_t K, int group) {
   LinearSplit p{1, 0};
@@ -775,7 +760,7 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   if (ti < 0 && part && sp.n_split > 1 && part_bytes >= linear_split_part_bytes(M, N, K, group) &&
       (M * N) % 4 == 0 && aligned(part, 16) && aligned(y, 16) && (!res || aligned(res, 16)) &&
       static_cast<int64_t>(sp.n_split) * M * N < (int64_t{1} << 31)) {
-    constexpr int T = 12;
+    constexpr int T = kSplitTile;
     const LinWsTile& t = kLinWsTiles[T];
     const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
     const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
@@ -801,7 +786,7 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   // projection of a 256-row chunk: 256x16384x3072 82 -> 69 us, x re-read over 4x fewer column tiles).
   if (ti < 0) {
     const int64_t wide = ((M + 63) / 64) * ((N + 255) / 256);
-    if (M <= 256 && wide >= 256) ti = 12;
+    if (M <= 256 && wide >= 256) ti = kSplitTile;
     else ti = ((M + 31) / 32) * ((N + 63) / 64) <= 768 ? 1 : 0;
   }
   const LinWsTile& t = kLinWsTiles[ti];
@@ -825,7 +810,7 @@ int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, c
   if (!oh || !ol) return Q4_ERR_NULL;
   const char* ov = getenv("Q4_LINEAR_CFG");
   if ((ov && *ov) || getenv("Q4_SWIGLU_UNFUSED")) return Q4_ERR_UNSUPPORTED;
-  constexpr LinWsTile t = kLinWsTiles[12];
+  constexpr LinWsTile t = kLinWsTiles[kSplitTile];
   const int64_t wide = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (!(M <= 256 && wide >= 256) || N % t.bn || (N / 2) % 32 || ol != oh + M * (N / 2)) return Q4_ERR_UNSUPPORTED;
   auto fn = q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, 1>;

@@ -187,8 +187,8 @@ def test_gemm_ws_config3(dev, M, N, K):
     assert (c.cpu().float() - c2).abs().max().item() <= 1e-2 * rms
 
 
-def test_gemm_ws_forced_splits_every_plain_tile(dev, monkeypatch):
-    """Every plain tile entry with K split 2, 3 and 5 ways (ranges not a multiple of the stage count)
+def test_gemm_ws_forced_splits_every_tile(dev, monkeypatch):
+    """Every tile entry with K split 2, 3 and 5 ways (ranges not a multiple of the stage count)
     at a ragged shape, and twice in a row into the same workspace: host fp32 reference each time."""
     from q4llm._lib import config_table
     M, N, K = 200, 300, 136 + 64 * 9
@@ -198,8 +198,6 @@ def test_gemm_ws_forced_splits_every_plain_tile(dev, monkeypatch):
     bar = 1e-2 * ref.pow(2).mean().sqrt().item()
     ws = torch.empty(5 * M * N * 4, dtype=torch.uint8, device=dev)
     for cfg, info in enumerate(config_table("gemm")):
-        if info[6]:
-            continue  # ping-pong entries do not split
         monkeypatch.setenv("Q4_GEMM_CFG", str(cfg))
         for S in (2, 3, 5):
             monkeypatch.setenv("Q4_GEMM_SPLIT", str(S))

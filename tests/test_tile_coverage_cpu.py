@@ -218,7 +218,7 @@ def test_mx_entries_cover_once(idx):
 
 
 # ------------------------------------------------------------------------------------------------
-# fp16 GEMM (csrc/gemm_f16.hip: gemm_f16_nt_kernel / gemm_f16_nt_pp_kernel)
+# fp16 GEMM (csrc/gemm_f16.hip: gemm_f16_nt_kernel)
 # ------------------------------------------------------------------------------------------------
 
 def swz(bk, r):
@@ -238,8 +238,8 @@ def tile_of(bid, tiles_m, tiles_n, remap):
 
 def gemm_split(cfg, M, N, K, force=None):
     """K split of a tile entry (csrc/gemm_f16.hip: gemm_split_plan): (n_split, nk_split)."""
-    bm, bn, wm, wn, nst, bk, pp, sp = cfg
-    if pp or N % 4 or M <= 1:
+    bm, bn, wm, wn, nst, bk, sp = cfg
+    if N % 4 or M <= 1:
         return 1, 0
     nk = cdiv(K, bk)
     tiles = cdiv(M, bm) * cdiv(N, bn)
@@ -254,9 +254,9 @@ def gemm_split(cfg, M, N, K, force=None):
 
 
 def replay_gemm(cfg, M, N, K, force_split=None):
-    """gemm_f16_nt_kernel / gemm_f16_nt_pp_kernel: workgroup -> (K range, tile) mapping, the direct
-    loads of one stage (lane offsets, row blocks, LDS slots), operand reads and epilogue stores."""
-    bm, bn, wm, wn, nst, bk, pp, sp = cfg
+    """gemm_f16_nt_kernel: workgroup -> (K range, tile) mapping, the direct loads of one stage (lane
+    offsets, row blocks, LDS slots), operand reads and epilogue stores."""
+    bm, bn, wm, wn, nst, bk, sp = cfg
     waves = wm * wn
     row_b = bk * 2
     rows_per_inst = 1024 // row_b
@@ -303,8 +303,6 @@ def replay_gemm(cfg, M, N, K, force_split=None):
                         blk = wave + j * waves
                         r = r0 + j * rows_per_j
                         real = blk < nrows // rows_per_inst
-                        if pp and not real:
-                            pytest.fail("ping-pong loads must divide evenly")
                         if not real:
                             continue  # spare instructions land in the junk area
                         # the chunk formula of row r gives the lane's chunk for every j
@@ -351,15 +349,14 @@ def test_gemm_entries_cover_once(idx):
     cfg = config_table("gemm")[idx]
     for (M, N, K) in ((300, 520, 200), (cfg[0] * 2, cfg[1] * 4, 512), (256, 3072, 8192)):
         replay_gemm(cfg, M, N, K)
-    if not cfg[6]:  # K splits (plain entries): forced counts, ragged K, and the automatic rule
-        for force in (2, 3, 5):
-            replay_gemm(cfg, 300, 520, 200 + 64 * 9, force)
-        replay_gemm(cfg, 256, 5120, 3072)
+    for force in (2, 3, 5):  # K splits: forced counts, ragged K, and the automatic rule
+        replay_gemm(cfg, 300, 520, 200 + 64 * 9, force)
+    replay_gemm(cfg, 256, 5120, 3072)
 
 
 def test_gemm_split_rule_fills_the_cus():
     """The automatic K split of the 256-row config-3 shapes on the pipelined 128x128 entry."""
-    cfg = next(c for c in config_table("gemm") if c[:6] == (128, 128, 2, 2, 4, 64) and c[7])
+    cfg = next(c for c in config_table("gemm") if c[:6] == (128, 128, 2, 2, 4, 64) and c[6])
     assert gemm_split(cfg, 256, 5120, 3072) == (3, 16)   # 80 tiles x 3
     assert gemm_split(cfg, 256, 3072, 8192) == (5, 26)   # 48 tiles x 5 (last range 24 steps)
     assert gemm_split(cfg, 256, 16384, 3072) == (1, 0)   # 256 tiles fill the CUs
