@@ -192,6 +192,20 @@ def replay_mx(cfg, N, K, G, pair, tiled):
                         stores[row] += 1
     assert (reads == 1).all(), "weight chunks read other than once"
     assert (stores == 1).all(), "outputs stored other than once"
+    if tiled and not pair:
+        # T16 scales: lane group b of row block rb loads 4 consecutive rows vs..vs+3 (one 8-byte load):
+        # aligned, inside one 16-row tile, and covering every used row of the block once
+        seen = np.zeros(N, np.int32)
+        for rb in range(n_rb):
+            for bb in range(4):
+                if 4 * bb >= rpb:
+                    continue
+                vs = rb * rpb + 4 * bb
+                assert vs % 4 == 0 and (vs >> 4) == ((vs + 3) >> 4)
+                for t in range(4):
+                    if 4 * bb + t < rpb and vs + t < N:
+                        seen[vs + t] += 1
+        assert (seen == 1).all(), "scale rows loaded other than once"
     # x prologue: thread tid owns 16-k block tid (< nblk)
     assert 64 * rbw * wpb >= n_tiles * (4 * G // 16)
 
