@@ -378,15 +378,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
   const int64_t mn = static_cast<int64_t>(M) * N;
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= mn) return;
-  float4 v = *reinterpret_cast<const float4*>(P + i);
-#pragma unroll 4
-  for (int s = 1; s < n_split; ++s) {
-    const float4 p = *reinterpret_cast<const float4*>(P + s * mn + i);
-    v.x += p.x;
-    v.y += p.y;
-    v.z += p.z;
-    v.w += p.w;
-  }
+  const float4 v = sum_partials4(reinterpret_cast<const float4*>(P + i), mn / 4, n_split);
   const int row = static_cast<int>(i / N), col = static_cast<int>(i - static_cast<int64_t>(row) * N);
   uint16_t* c = Cm + static_cast<int64_t>(row) * ldc + col;
   if (kPacked) {

@@ -15,6 +15,19 @@
 namespace q4 {
 namespace {
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+// 16 bytes at byte offset off of the buffer; out of range (e.g. 0x80000000): zeros, no memory access.
+// The whole vector is bit-cast: bit-casting single elements of the loaded vector compiled to four
+// copies of element 0 with this compiler.
+__device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 f = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return make_float4(f.x, f.y, f.z, f.w);
+}
+
 // rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
 // mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w. Rows of at
 // most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight; the
@@ -37,34 +50,51 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
   float4 v[kV], wv[kV];
   float s = 0.0f;
   if (vec) {
+    // Buffer loads: float4s past the row come back as zeros without a branch, so every load of the
+    // row, its norm weights and (n_split > 0) its K-split partials is in flight before the first use.
+    const __amdgpu_buffer_rsrc_t xres = row_rsrc(xr, static_cast<uint32_t>(D) * 4u);
+    const __amdgpu_buffer_rsrc_t wres = row_rsrc(w, static_cast<uint32_t>(D) * 4u);
 #pragma unroll
-    for (int i = 0; i < kV; ++i) {
-      const int64_t j = threadIdx.x + i * 256;
-      v[i] = j < D / 4 ? reinterpret_cast<const float4*>(xr)[j] : make_float4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < kV; ++i) v[i] = load_f4(xres, (threadIdx.x + i * 256) * 16u);
 #pragma unroll
-    for (int i = 0; i < kV; ++i) {
-      const int64_t j = threadIdx.x + i * 256;
-      wv[i] = j < D / 4 ? reinterpret_cast<const float4*>(w)[j] : make_float4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < kV; ++i) wv[i] = load_f4(wres, (threadIdx.x + i * 256) * 16u);
     if (n_split > 0) {
-      const int64_t plane = M * D / 4;
-      const float4* pr = reinterpret_cast<const float4*>(psum) + row * (D / 4);
+      // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row, the sums run
+      // in ascending split order, as in linear_reduce_kernel
+      constexpr int kPb = 6;
+      const uint32_t row_bytes = static_cast<uint32_t>(D) * 4u;
+      const uint32_t plane_bytes = static_cast<uint32_t>(M * D) * 4u;
+      const __amdgpu_buffer_rsrc_t pres = row_rsrc(psum, plane_bytes * static_cast<uint32_t>(n_split));
+      const uint32_t prow = static_cast<uint32_t>(row) * row_bytes;
+      float4 pb[kV][kPb];
+#pragma unroll
+      for (int sp = 0; sp < kPb; ++sp)
+#pragma unroll
+        for (int i = 0; i < kV; ++i)
+          pb[i][sp] = load_f4(pres, sp < n_split && (threadIdx.x + i * 256) * 16u < row_bytes
+                                        ? sp * plane_bytes + prow + (threadIdx.x + i * 256) * 16u
+                                        : 0x80000000u);
 #pragma unroll
       for (int i = 0; i < kV; ++i) {
         const int64_t j = threadIdx.x + i * 256;
-        if (j < D / 4) {
-          float4 a = pr[j];
-          for (int sp = 1; sp < n_split; ++sp) {
-            const float4 b = pr[sp * plane + j];
-            a.x += b.x;
-            a.y += b.y;
-            a.z += b.z;
-            a.w += b.w;
+        float4 a = pb[i][0];
+#pragma unroll
+        for (int sp = 1; sp < kPb; ++sp)
+          if (sp < n_split) {
+            a.x += pb[i][sp].x;
+            a.y += pb[i][sp].y;
+            a.z += pb[i][sp].z;
+            a.w += pb[i][sp].w;
           }
-          v[i] = make_float4(v[i].x + a.x, v[i].y + a.y, v[i].z + a.z, v[i].w + a.w);
-          reinterpret_cast<float4*>(const_cast<float*>(xr))[j] = v[i];
+        for (int sp = kPb; sp < n_split; ++sp) {
+          const float4 c = load_f4(pres, j * 16 < row_bytes ? sp * plane_bytes + prow + j * 16u : 0x80000000u);
+          a.x += c.x;
+          a.y += c.y;
+          a.z += c.z;
+          a.w += c.w;
         }
+        v[i] = make_float4(v[i].x + a.x, v[i].y + a.y, v[i].z + a.z, v[i].w + a.w);
+        if (j < D / 4) reinterpret_cast<float4*>(const_cast<float*>(xr))[j] = v[i];
       }
     }
 #pragma unroll
@@ -183,16 +213,10 @@ __global__ __launch_bounds__(256) void rope_kv4_kernel(float* __restrict__ qkv, 
   float* row = qkv + (static_cast<int64_t>(c) * heads + head) * hd;
   float4 x1, x2;
   if (n_split > 0) {
-    const int64_t plane = static_cast<int64_t>(C) * heads * hd;
+    const int64_t plane4 = static_cast<int64_t>(C) * heads * hd / 4;  // hd % 4 == 0
     const float* pr = part + (row - qkv);
-    x1 = *reinterpret_cast<const float4*>(pr + d);
-    x2 = *reinterpret_cast<const float4*>(pr + d + half);
-    for (int sp = 1; sp < n_split; ++sp) {
-      const float4 b1 = *reinterpret_cast<const float4*>(pr + sp * plane + d);
-      const float4 b2 = *reinterpret_cast<const float4*>(pr + sp * plane + d + half);
-      x1 = make_float4(x1.x + b1.x, x1.y + b1.y, x1.z + b1.z, x1.w + b1.w);
-      x2 = make_float4(x2.x + b2.x, x2.y + b2.y, x2.z + b2.z, x2.w + b2.w);
-    }
+    x1 = sum_partials4(reinterpret_cast<const float4*>(pr + d), plane4, n_split);
+    x2 = sum_partials4(reinterpret_cast<const float4*>(pr + d + half), plane4, n_split);
   } else {
     x1 = *reinterpret_cast<const float4*>(row + d);
     x2 = *reinterpret_cast<const float4*>(row + d + half);
@@ -404,7 +428,9 @@ int rmsnorm_planes(float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t
   if (!x || !w || !xh || !xl) return Q4_ERR_NULL;
   if (M <= 0 || D <= 0 || D % 8) return Q4_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
-  if (n_split > 0 && (!part || !aligned(part, 16) || !rmsnorm_takes_partials(D))) return Q4_ERR_UNSUPPORTED;
+  if (n_split > 0 && (!part || !aligned(part, 16) || !rmsnorm_takes_partials(D) ||
+                      static_cast<int64_t>(n_split) * M * D * 4 >= (int64_t{1} << 31)))
+    return Q4_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
                      nullptr, xh, xl, part, n_split);
   return launch_status();
@@ -414,6 +440,7 @@ int rmsnorm_row_partials(float* x, const float* w, float* out, int64_t M, int64_
                          const float* part, int n_split, hipStream_t st) {
   if (!x || !w || !out || !row || !part) return Q4_ERR_NULL;
   if (M <= 0 || D <= 0 || n_split <= 0 || !rmsnorm_takes_partials(D)) return Q4_ERR_SHAPE;
+  if (static_cast<int64_t>(n_split) * M * D * 4 >= (int64_t{1} << 31)) return Q4_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || !aligned(part, 16)) return Q4_ERR_ALIGN;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, M, D, eps, row, nullptr, nullptr, part,
                      n_split);

@@ -61,6 +61,34 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
+// p[0] + p[stride] + ... + p[(n - 1) stride] (n >= 1), added in ascending order, so the result has the
+// same bits as a plain loop; the first kBatch loads are issued together before any is waited for (a
+// loop over a runtime count would wait for each load before issuing the next).
+__device__ __forceinline__ float4 sum_partials4(const float4* __restrict__ p, int64_t stride, int n) {
+  constexpr int kBatch = 8;
+  float4 b[kBatch];
+#pragma unroll
+  for (int s = 0; s < kBatch; ++s)
+    if (s < n) b[s] = p[s * stride];
+  float4 a = b[0];
+#pragma unroll
+  for (int s = 1; s < kBatch; ++s)
+    if (s < n) {
+      a.x += b[s].x;
+      a.y += b[s].y;
+      a.z += b[s].z;
+      a.w += b[s].w;
+    }
+  for (int s = kBatch; s < n; ++s) {
+    const float4 c = p[s * stride];
+    a.x += c.x;
+    a.y += c.y;
+    a.z += c.z;
+    a.w += c.w;
+  }
+  return a;
+}
+
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64); every lane of the
 // group receives the total. Uses cross-lane permutes; the summation tree is fixed, so results are
 // deterministic.

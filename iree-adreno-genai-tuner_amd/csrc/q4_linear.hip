@@ -622,14 +622,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float4* __rest
                                                             int64_t n, int n_split) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
-  float4 a = P[i];
-  for (int s = 1; s < n_split; ++s) {
-    const float4 b = P[s * n + i];
-    a.x += b.x;
-    a.y += b.y;
-    a.z += b.z;
-    a.w += b.w;
-  }
+  float4 a = sum_partials4(P + i, n, n_split);
   if (R) {
     const float4 r = R[i];
     a = make_float4(r.x + a.x, r.y + a.y, r.z + a.z, r.w + a.w);
