@@ -260,9 +260,10 @@ int argmax_f32(const float* logits, int64_t V, int32_t* out, void* workspace, si
  * decode_logits_l{L}, scripts/llm/export_llama.py:1-10,35-49; LlamaQ4.step llama_q4.py:199-239)
  * ------------------------------------------------------------------------------------------- */
 
-/* Optional T16 copies (q4_t16_pack) of a weight for the decode GEMVs: tiles and tile scales, both
- * NULL when absent (decode then reads the reference layout). wqkv takes Q4_PAIR_ROPE pairing,
- * wgu Q4_PAIR_SWIGLU, wo, wdown and the LM head Q4_PAIR_NONE. */
+/* Optional T16 copies (q4_t16_pack) of a weight for the decode GEMVs, also read by the prefill
+ * GEMM's 64x256 tile: tiles and tile scales, both NULL when absent (decode and prefill then read
+ * the reference layout). wqkv takes Q4_PAIR_ROPE pairing, wgu Q4_PAIR_SWIGLU, wo, wdown and the
+ * LM head Q4_PAIR_NONE. */
 typedef struct q4llm_t16 {
   const void* tiles;
   const void* scales;
@@ -365,7 +366,7 @@ int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
  *   q4_gemv_mx_config_info: row blocks per workgroup, waves per row block, tiles per wave, used rows
  *                           per 16-row block, grid-stride (q4_gemv_mx_num_configs entries)
  *   gemm_f16_config_info:   BM, BN, wave rows, wave columns, stages, BK, pipelined substeps
- *   q4_linear_ws_config_info: BM, BN, wave rows, wave columns, stages, k-split */
+ *   q4_linear_ws_config_info: BM, BN, wave rows, wave columns, stages, k-split, pipelined (0/1) */
 int q4_gemv_config_info(int cfg, int* info);
 int q4_gemv_mx_num_configs(void);
 int q4_gemv_mx_config_info(int cfg, int* info);

@@ -62,14 +62,24 @@ size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group);
 // linear_split_part_bytes, 16-byte aligned) it may split K and reduce the partials in a second kernel.
 // With `deferred` not null, a K split leaves its partials in `part` unreduced and sets *deferred to the
 // number of splits (0 when the result went to y); the caller's next kernel then completes y.
+// The decode T16 copy of the same weight (q4_t16_pack: tiles, scales, and the pairing and head size it
+// was packed with), which the 64x256 tile reads instead of qw / sc when it takes the projection: its
+// 1 KB loads then touch 16 cache lines instead of 32.
+struct T16Src {
+  const void* tiles;
+  const uint16_t* scales;
+  int pairing, head_dim;
+};
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st,
-                     float* part = nullptr, size_t part_bytes = 0, int* deferred = nullptr);
+                     float* part = nullptr, size_t part_bytes = 0, int* deferred = nullptr,
+                     const T16Src* t16 = nullptr);
 // The gate/up projection with silu(gate) * up written as the [M, N / 2] planes oh / ol (ol = oh + M N / 2)
 // of the down projection; Q4_ERR_UNSUPPORTED when the shape does not take the fused tile (the caller then
 // runs q4_linear_planes + silu_mul_planes).
 int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
-                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st);
+                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st,
+                            const T16Src* t16 = nullptr);
 // rmsnorm_f32 of M rows (no row selection), written as planes. With n_split > 0 each row of x is first
 // completed with the K-split partials `part` of the projection that produced it (x += sum of n_split
 // [M, D] planes, written back to x); requires rmsnorm_takes_partials(D).

@@ -354,13 +354,22 @@ __device__ __forceinline__ float silu_mul_exact(float g, float u) {
 // Split over K (n_split > 1, EPI = 0): workgroup s * tiles + t takes output tile t over the 64-k stages
 // [s * nk_split, (s + 1) * nk_split) (whole groups) and writes its sum, without the residual, to the
 // partial buffer P[s] ([M, N] fp32 each); linear_reduce_kernel then adds the residual and the partials.
-template <int BM, int BN, int WM, int WN, int NST, int KS, int EPI = 0>
+// T16 (the decode GEMV's layout, q4_t16.hip; pipelined tile only): QW and SC are the T16 tiles and
+// scales of the weight, whose rows sit in the layout's virtual order (t16_pair / t16_hd: the pairing
+// and head size it was packed with). Columns are virtual rows: a 64-k stage of 32 of them is half of
+// each 64-byte row of two 16-row tiles (16 cache lines per 1 KB load instead of 32 in the reference
+// layout), a group's scales of a tile are 32 contiguous bytes, and the epilogue writes each virtual
+// column to its weight row (SwiGLU: gate and up of a pair sit 8 columns apart, exchanged by DPP).
+template <int BM, int BN, int WM, int WN, int NST, int KS, int EPI = 0, bool PIPE = false, bool T16 = false>
 __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
     const uint16_t* __restrict__ SC, float* Y, const float* R, int M, int N, int K, int group, int tiles_n,
-    int n_split = 1, int nk_split = 0, float* __restrict__ P = nullptr) {
+    int n_split = 1, int nk_split = 0, float* __restrict__ P = nullptr, int t16_pair = 0, int t16_hd = 0) {
   using G = LinWsCfg<BM, BN, WM, WN, NST, KS>;
-  static_assert(EPI == 0 || (G::TN % 2 == 0 && G::WTN % 64 == 0 && BN % 64 == 0), "SwiGLU pairs tiles 2j, 2j + 1");
+  static_assert(EPI == 0 || T16 || (G::TN % 2 == 0 && G::WTN % 64 == 0 && BN % 64 == 0),
+                "SwiGLU pairs tiles 2j, 2j + 1");
+  static_assert(!T16 || (PIPE && BN % 128 == 0 && (2 * (BN / 128) + G::kWaves - 1) / G::kWaves == G::kSI),
+                "T16: the pipelined loop, scale loads of 128 columns in the reference layout's count");
   // weight row of virtual column v
   auto phys = [&](int v) -> int {
     if constexpr (EPI == 0) {
@@ -387,8 +396,15 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
   const uint32_t xbytes = static_cast<uint32_t>(M) * K * 2u;
   const __amdgpu_buffer_rsrc_t hr = make_rsrc(XH, xbytes);
   const __amdgpu_buffer_rsrc_t lr = make_rsrc(XL, xbytes);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(QW, static_cast<uint32_t>(N) * (K / 2));
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(SC, (static_cast<uint32_t>(N) * spr * 2u + 3u) & ~3u);
+  // T16 geometry: 16-row tiles of nseg 128-k segments (K padded to 4 groups); scales per tile in
+  // [n_tiles][4 groups][16 rows]
+  const int t16_tiles_k = (K + 4 * group - 1) / (4 * group);
+  const int t16_nseg = t16_tiles_k * group / 32;
+  const int n_t16 = t16_pair == 0 ? (N + 15) / 16 : N / 16;
+  const __amdgpu_buffer_rsrc_t wr =
+      T16 ? make_rsrc(QW, static_cast<uint32_t>(n_t16) * t16_nseg * 1024u) : make_rsrc(QW, static_cast<uint32_t>(N) * (K / 2));
+  const __amdgpu_buffer_rsrc_t sr = T16 ? make_rsrc(SC, static_cast<uint32_t>(n_t16) * t16_tiles_k * 128u)
+                                        : make_rsrc(SC, (static_cast<uint32_t>(N) * spr * 2u + 3u) & ~3u);
 
   // x planes: instruction j fills rows 8b..8b+7 (b = wave + j * kWaves < BM / 8) of a 128-byte-row
   // plane; the lane for slot (lane % 8) of row r = 8b + lane / 8 fetches chunk (lane % 8) ^ ((r >> 1) & 7).
@@ -414,7 +430,15 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const int b = wave + j * G::kWaves;
     const int r = 32 * b + (lane >> 1);
     wreal[j] = b < BN / 32;
-    woff[j] = wreal[j] && n0 + r < N ? static_cast<uint32_t>(phys(n0 + r)) * (K / 2) + (lane & 1) * 16u : kOOBw;
+    if constexpr (T16) {
+      // lane -> (tile half lane / 32, row (lane % 32) / 2, 16-byte piece lane % 2) of 32 virtual rows
+      const int t = (n0 + 32 * b) / 16 + (lane >> 5);
+      woff[j] = wreal[j] && t < n_t16
+                    ? static_cast<uint32_t>(t) * t16_nseg * 1024u + ((lane & 31) >> 1) * 64u + (lane & 1) * 16u
+                    : kOOBw;
+    } else {
+      woff[j] = wreal[j] && n0 + r < N ? static_cast<uint32_t>(phys(n0 + r)) * (K / 2) + (lane & 1) * 16u : kOOBw;
+    }
   }
   unsigned char* junk = lds + NST * G::kStage;
   // Every step issues the same loads (steps past K load zeros into a free stage), so the number of
@@ -423,30 +447,47 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
   const int nk = K / 64;
   const int kt_begin = n_split > 1 ? ksp * nk_split : 0;
   const int kt_end = n_split > 1 ? min(nk, kt_begin + nk_split) : nk;
-  auto issue = [&](int kt, int stage) {
+  // Load idx (0 <= idx < kLPW, a constant after unrolling) of K step kt into `stage`: the x_hi and x_lo
+  // rows of instruction idx / 2 (idx < 2 kAI), then the weight rows, then the scale words.
+  auto issue_one = [&](int idx, int kt, int stage) {
     const int k0 = kt * 64;
     const bool kin = kt < kt_end;
     unsigned char* sh = lds + stage * G::kStage;
     unsigned char* sl = sh + BM * G::kXRow;
     unsigned char* sw = sl + BM * G::kXRow;
-#pragma unroll
-    for (int j = 0; j < G::kAI; ++j) {
+    if (idx < 2 * G::kAI) {
+      const int j = idx / 2;
       const uint32_t off = kin && xoff[j] != kOOBw ? xoff[j] + k0 * 2u : kOOBw;
-      load_lds16(hr, xreal[j] ? sh + (wave + j * G::kWaves) * 1024 : junk, off);
-      load_lds16(lr, xreal[j] ? sl + (wave + j * G::kWaves) * 1024 : junk, off);
-    }
-#pragma unroll
-    for (int j = 0; j < G::kBI; ++j)
+      if (idx % 2 == 0) load_lds16(hr, xreal[j] ? sh + (wave + j * G::kWaves) * 1024 : junk, off);
+      else load_lds16(lr, xreal[j] ? sl + (wave + j * G::kWaves) * 1024 : junk, off);
+    } else if (idx < 2 * G::kAI + G::kBI) {
+      const int j = idx - 2 * G::kAI;
+      const uint32_t kofs = T16 ? static_cast<uint32_t>(kt >> 1) * 1024u + (kt & 1) * 32u : static_cast<uint32_t>(k0 / 2);
       load_lds16(wr, wreal[j] ? sw + (wave + j * G::kWaves) * 1024 : junk,
-                 kin && woff[j] != kOOBw ? woff[j] + k0 / 2 : kOOBw);
-    // Scales: instruction i = wave + j * kWaves (< 2 kSBlk) fills slot i / kSBlk (the step's first or
-    // last group; a 64-k step touches at most two groups of >= 32) for the 64 columns of block
-    // i % kSBlk: lane -> column, the aligned dword holding its fp16 scale (the buffer range is rounded
-    // up to 4 bytes; device allocations are 256-byte granular). Spare instructions fill the junk area.
-    unsigned char* ss = sw + BN * G::kWRow;
-    const int g0 = k0 >> gshift, g1 = (k0 + 63) >> gshift;
-#pragma unroll
-    for (int j = 0; j < G::kSI; ++j) {
+                 kin && woff[j] != kOOBw ? woff[j] + kofs : kOOBw);
+    } else if constexpr (T16) {
+      // Scales: instruction i = wave + j * kWaves (< 2 BN / 128) fills slot i / (BN / 128) (the step's
+      // first or last group) for the 128 virtual columns of part i % (BN / 128): lane -> rows 2 (lane % 8)
+      // and + 1 of tile lane / 8 of the part, stored as fp16 in column order.
+      unsigned char* ss = sw + BN * G::kWRow;
+      const int g0 = k0 >> gshift, g1 = (k0 + 63) >> gshift;
+      const int j = idx - 2 * G::kAI - G::kBI;
+      const int i = wave + j * G::kWaves;
+      constexpr int kParts = BN / 128;
+      const bool real = i < 2 * kParts;
+      const int slot = i / kParts, part = i - slot * kParts;
+      const int t = n0 / 16 + part * 8 + (lane >> 3);
+      const int g = slot ? g1 : g0;
+      const uint32_t e = ((static_cast<uint32_t>(t) * t16_tiles_k + (g >> 2)) * 4u + (g & 3)) * 16u + 2u * (lane & 7);
+      load_lds4(sr, real ? ss + slot * (BN * 2) + part * 256 : junk, real && kin && t < n_t16 ? e * 2u : kOOBw);
+    } else {
+      // Scales: instruction i = wave + j * kWaves (< 2 kSBlk) fills slot i / kSBlk (the step's first or
+      // last group; a 64-k step touches at most two groups of >= 32) for the 64 columns of block
+      // i % kSBlk: lane -> column, the aligned dword holding its fp16 scale (the buffer range is rounded
+      // up to 4 bytes; device allocations are 256-byte granular). Spare instructions fill the junk area.
+      unsigned char* ss = sw + BN * G::kWRow;
+      const int g0 = k0 >> gshift, g1 = (k0 + 63) >> gshift;
+      const int j = idx - 2 * G::kAI - G::kBI;
       const int i = wave + j * G::kWaves;
       const bool real = i < 2 * G::kSBlk;
       const int slot = i / G::kSBlk, blk = i - slot * G::kSBlk;
@@ -455,6 +496,10 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
       load_lds4(sr, real ? ss + (slot * G::kSBlk + blk) * 256 : junk,
                 real && kin && col < N ? (e >> 1) * 4u : kOOBw);
     }
+  };
+  auto issue = [&](int kt, int stage) {
+#pragma unroll
+    for (int idx = 0; idx < G::kLPW; ++idx) issue_one(idx, kt, stage);
   };
 
   auto scale_elem = [&](int j, int g) -> uint32_t {
@@ -548,9 +593,139 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
       }
     }
   };
+  if constexpr (!PIPE) {
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s) issue(kt_begin + s, (kt_begin + s) % NST);
-  for (int kt = kt_begin; kt < kt_end; ++kt) step(kt);
+    for (int s = 0; s < NST - 1; ++s) issue(kt_begin + s, (kt_begin + s) % NST);
+    for (int kt = kt_begin; kt < kt_end; ++kt) step(kt);
+  } else {
+    // Software pipeline (one wave group): the operands of each 16-k step are read into one of two
+    // fragment sets while the MFMAs of the previous one run from the other, so the LDS reads overlap
+    // the matrix core instead of preceding it. K step l of this workgroup (l = kt - kt_begin) sits in
+    // buffer l % NST. The one barrier per step comes after this wave's reads of step l and before its
+    // last MFMAs: past it every wave is done with buffer l % NST, and step l + 1 has landed, whose
+    // first 16-k operands are then read while the last MFMAs of step l run. Step l issues the loads of
+    // step l + NST - 1 into the buffer freed at the previous barrier (step l - 1's; buffer NST - 1 is
+    // still unused at l = 0), spread over its first three 16-k steps, one between MFMAs. Every step
+    // issues the same kLPW loads (past kt_end: zeros), so the vmcnt counts below are constants.
+    static_assert(KS == 1, "the pipelined loop runs one wave group over all four 16-k steps");
+    constexpr int KK = 4;
+    const int nl = kt_end - kt_begin;
+    half8 fh[2][G::TM], fl[2][G::TM];
+    uint32_t fw[2][G::TN];
+    uint32_t sw0[G::TN], sw1[G::TN];  // scale words of the step's slots 0 and 1
+    const F16Magic mg = f16_magic();
+    auto read_sub = [&](int l, int kk, int set) {
+      const unsigned char* sh = lds + (l % NST) * G::kStage;
+      const unsigned char* sl = sh + BM * G::kXRow;
+      const unsigned char* sw = sl + BM * G::kXRow;
+      const int c = 2 * kk + (lane >> 5);  // this lane's 8-k chunk of the 16-k step
+      const int xs = (c ^ ((lane >> 1) & 7)) << 4;
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i) {
+        fh[set][i] = *reinterpret_cast<const half8*>(sh + (arow + 32 * i) * G::kXRow + xs);
+        fl[set][i] = *reinterpret_cast<const half8*>(sl + (arow + 32 * i) * G::kXRow + xs);
+      }
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) fw[set][j] = *reinterpret_cast<const uint32_t*>(sw + (brow + 32 * j) * G::kWRow + 4 * c);
+    };
+    auto read_scales = [&](int l) {
+      const unsigned char* ss = lds + (l % NST) * G::kStage + 2 * BM * G::kXRow + BN * G::kWRow;
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) {
+        const int cl = wn * G::WTN + j * 32 + (lane & 31);
+        if constexpr (T16) {
+          sw0[j] = *reinterpret_cast<const uint16_t*>(ss + cl * 2);
+          sw1[j] = *reinterpret_cast<const uint16_t*>(ss + BN * 2 + cl * 2);
+        } else {
+          sw0[j] = *reinterpret_cast<const uint32_t*>(ss + cl * 4);
+          sw1[j] = *reinterpret_cast<const uint32_t*>(ss + G::kSBlk * 256 + cl * 4);
+        }
+      }
+    };
+    // The MFMAs of 16-k step q from fragment set `set` (x_hi products of every tile, then x_lo, so
+    // consecutive MFMAs write different tiles), with loads [q kLPW / 3, (q + 1) kLPW / 3) of K step
+    // kt_begin + ld (q < 3) placed one after each of the first MFMAs.
+    auto mfma_sub = [&](int set, int q, int ld) {
+      half8 fb[G::TN];
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j) fb[j] = nibbles_to_half8(fw[set][j], mg);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[set][i], fb[j], part[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j)
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[set][i], fb[j], part[i][j], 0, 0, 0);
+      if (q < KK - 1) {
+#pragma unroll
+        for (int idx = q * G::kLPW / (KK - 1); idx < (q + 1) * G::kLPW / (KK - 1); ++idx)
+          issue_one(idx, kt_begin + ld, ld % NST);
+        constexpr int kMaxLoads = (G::kLPW + KK - 2) / (KK - 1);
+#pragma unroll
+        for (int l = 0; l < kMaxLoads; ++l) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one vector-memory load
+        }
+      }
+    };
+    // Group end after 16-k step q of K step l: scale this lane's group sums into the outputs.
+    auto scale_end = [&](int l, int q) {
+      const int k0 = (kt_begin + l) * 64, k = k0 + 16 * q;
+      if (((k + 16) & (group - 1)) == 0) {
+        const int g = k >> gshift;
+        const bool second = g != (k0 >> gshift);
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+          const uint32_t v = second ? sw1[j] : sw0[j];
+          const float sc = half_bits_to_float(static_cast<uint16_t>(T16 ? v : v >> (16 * (scale_elem(j, g) & 1))));
+#pragma unroll
+          for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              acc[i][j][e] = fmaf(part[i][j][e], sc, acc[i][j][e]);
+              part[i][j][e] = 0.0f;
+            }
+        }
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue(kt_begin + s, s);
+    wait_vmcnt<(NST - 2) * G::kLPW>();  // step 0 landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_sub(0, 0, 0);
+    for (int l = 0; l < nl; ++l) {
+      const int ld = l + NST - 1;
+#pragma unroll
+      for (int kk = 0; kk < KK - 1; ++kk) {
+        read_sub(l, kk + 1, (kk + 1) & 1);
+        if (kk == 0) read_scales(l);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_sub(kk & 1, kk, ld);
+        __builtin_amdgcn_sched_barrier(0);
+        scale_end(l, kk);
+      }
+      if (l + 1 < nl) {
+        // this wave's loads of step l + 1 landed (steps up to l + NST - 1 issued); its reads of step l
+        // done (lgkmcnt(0)) before the barrier frees the buffer
+        wait_vmcnt<(NST - 2) * G::kLPW>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        read_sub(l + 1, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_sub(1, KK - 1, -1);
+      __builtin_amdgcn_sched_barrier(0);
+      scale_end(l, KK - 1);
+    }
+    wait_vmcnt<0>();  // the last steps' (zero) loads have landed before the waves exit
+  }
 
   if constexpr (KS > 1) {
     // k-split: wave groups 1..KS-1 hand their sums to group 0 through LDS (the stage memory; the
@@ -582,7 +757,28 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
           for (int e = 0; e < 16; ++e) acc[i][j][e] += *slot(g2, i, j, e);
   }
 
-  if constexpr (EPI == 1) {
+  if constexpr (EPI == 1 && T16) {
+    // virtual column c of a 16-column group: gate row 8 (c / 16) + c % 8 for c % 16 < 8, its up row 8
+    // columns later; lane l (column l % 32) swaps with lane l ^ 8 (DPP row rotate by 8)
+    const int I = N >> 1;
+    uint16_t* oh = reinterpret_cast<uint16_t*>(Y);
+    uint16_t* ol = oh + static_cast<int64_t>(M) * I;
+#pragma unroll
+    for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < G::TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float g = acc[i][j][e];
+          const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, g), 0x128, 0xF, 0xF, false));
+          const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+          const int vc = n0 + wn * G::WTN + j * 32 + (lane & 31);
+          const int pr = 8 * (vc >> 4) + (vc & 7);
+          if ((lane & 8) == 0 && row < M && pr < I)
+            store_x_planes(oh, ol, static_cast<int64_t>(row) * I + pr, silu_mul_exact(g, u));
+        }
+    return;
+  } else if constexpr (EPI == 1) {
     const int I = N >> 1;
     uint16_t* oh = reinterpret_cast<uint16_t*>(Y);
     uint16_t* ol = oh + static_cast<int64_t>(M) * I;
@@ -607,7 +803,15 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-        const int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+        int col = n0 + wn * G::WTN + j * 32 + (lane & 31);
+        if constexpr (T16) {
+          if (t16_pair == Q4_PAIR_ROPE) {
+            // virtual column -> pair p = 8 (c / 16) + c % 8, rows (head, d) and (head, d + hd / 2)
+            const int pr = 8 * (col >> 4) + (col & 7), hh = t16_hd >> 1, sh = __builtin_ctz(hh);
+            const int head = pr >> sh;
+            col = pr < (N >> 1) ? head * t16_hd + (pr - (head << sh)) + ((col & 8) ? hh : 0) : N;
+          }
+        }
         if (row < M && col < N) {
           const int64_t o = static_cast<int64_t>(row) * N + col;
           if (n_split > 1) P[static_cast<int64_t>(ksp) * M * N + o] = acc[i][j][e];
@@ -632,6 +836,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float4* __rest
 
 struct LinWsTile {
   int bm, bn, wm, wn, nst, ks;
+  bool pipe;
 };
 // Explicit tile list (index stable for Q4_LINEAR_CFG sweeps): the entries the rules below pick. Swept
 // and removed (slower on every 3B prefill shape at M = 128, 256 and 1024): 4-wave 64x64, 32x64 and
@@ -641,15 +846,22 @@ struct LinWsTile {
 constexpr LinWsTile kLinWsTiles[] = {
     {64, 64, 2, 2, 4, 1},    // 0: 4 waves of 32x32, 4 stages (77 KB)
     {32, 64, 1, 2, 4, 2},    // 1: 4 waves: 2 tiles of 32x32, each k-split over 2 waves (52 KB)
-    {64, 256, 2, 4, 4, 1},   // 2: 8 waves of 32x64: one workgroup per CU for 256-row chunks, and the K split
+    {64, 256, 2, 4, 4, 1, true},  // 2: 8 waves of 32x64, software-pipelined: one workgroup per CU for
+                                  // 256-row chunks, and the K split
 };
 constexpr int kSplitTile = 2;  // the K-split tile (linear_split_plan) and the SwiGLU-epilogue tile
 using LinWsFn = void (*)(const uint16_t*, const uint16_t*, const int32_t*, const uint16_t*, float*, const float*, int,
-                         int, int, int, int, int, int, float*);
+                         int, int, int, int, int, int, float*, int, int);
 template <int I>
 constexpr LinWsFn lin_ws_fn() {
   constexpr LinWsTile t = kLinWsTiles[I];
-  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>;
+  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, 0, t.pipe>;
+}
+// the K-split / SwiGLU tile with the weight in the T16 layout (EPI 0 or 1)
+template <int EPI>
+constexpr LinWsFn lin_ws_t16_fn() {
+  constexpr LinWsTile t = kLinWsTiles[kSplitTile];
+  return q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, EPI, true, true>;
 }
 template <int I>
 constexpr size_t lin_ws_lds() {
@@ -658,6 +870,21 @@ constexpr size_t lin_ws_lds() {
 }
 constexpr LinWsFn kLinWsFns[] = {lin_ws_fn<0>(), lin_ws_fn<1>(), lin_ws_fn<2>()};
 constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>()};
+static_assert(kLinWsTiles[kSplitTile].pipe && kLinWsTiles[kSplitTile].ks == 1, "the T16 variants need the pipelined loop");
+
+// A T16 source the K-split tile can read: both pointers, a group the layout takes, whole 16-row tiles
+// for the paired orders, 16-byte aligned tiles (Q4_PREFILL_REF_LAYOUT set: the reference layout).
+bool t16_usable(const T16Src* t, int64_t N, int group, int pairing_needed) {
+  if (!t || !t->tiles || !t->scales || getenv("Q4_PREFILL_REF_LAYOUT")) return false;
+  if ((group != 32 && group != 128) || !aligned(t->tiles, 16) || !aligned(t->scales, 4)) return false;
+  if (pairing_needed >= 0 && t->pairing != pairing_needed) return false;
+  if (t->pairing == Q4_PAIR_SWIGLU) return pairing_needed == Q4_PAIR_SWIGLU && N % 16 == 0;
+  if (t->pairing == Q4_PAIR_ROPE) {
+    const int hh = t->head_dim / 2;
+    return N % 16 == 0 && t->head_dim > 0 && hh % 8 == 0 && (hh & (hh - 1)) == 0 && N % t->head_dim == 0;
+  }
+  return t->pairing == Q4_PAIR_NONE;
+}
 static_assert(sizeof(kLinWsFns) / sizeof(kLinWsFns[0]) == sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]),
               "one kernel per tile entry");
 constexpr int kNumLinWs = sizeof(kLinWsTiles) / sizeof(kLinWsTiles[0]);
@@ -691,8 +918,8 @@ int q4_linear_ws_num_tiles() { return kNumLinWs; }
 int q4_linear_ws_tile_info(int i, int* out) {
   if (i < 0 || i >= kNumLinWs) return Q4_ERR_RANGE;
   const LinWsTile& t = kLinWsTiles[i];
-  const int v[6] = {t.bm, t.bn, t.wm, t.wn, t.nst, t.ks};
-  for (int j = 0; j < 6; ++j) out[j] = v[j];
+  const int v[7] = {t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, t.pipe ? 1 : 0};
+  for (int j = 0; j < 7; ++j) out[j] = v[j];
   return Q4_OK;
 }
 
@@ -742,7 +969,7 @@ size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group) {
 // k-split tile while it gives at most 768 workgroups, else 64x64. Q4_LINEAR_CFG overrides (no K split).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st, float* part,
-                     size_t part_bytes, int* deferred) {
+                     size_t part_bytes, int* deferred, const T16Src* t16) {
   if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
   if (!y) return Q4_ERR_NULL;
   if (deferred) *deferred = 0;
@@ -757,12 +984,16 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
     const LinWsTile& t = kLinWsTiles[T];
     const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
     const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
+    const bool use_t16 = t16_usable(t16, N, group, -1);
+    const LinWsFn fn = use_t16 ? lin_ws_t16_fn<0>() : kLinWsFns[T];
     if (kLinWsLds[T] > 64 * 1024) {
-      Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kLinWsFns[T]),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[T])));
+      Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(kLinWsLds[T])));
     }
-    hipLaunchKernelGGL(kLinWsFns[T], dim3(tiles * sp.n_split), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[T], st, xh,
-                       xl, qw, sc, y, res, (int)M, (int)N, (int)K, group, tiles_n, sp.n_split, sp.nk_split, part);
+    hipLaunchKernelGGL(fn, dim3(tiles * sp.n_split), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[T], st, xh, xl,
+                       use_t16 ? static_cast<const int32_t*>(t16->tiles) : qw, use_t16 ? t16->scales : sc, y, res,
+                       (int)M, (int)N, (int)K, group, tiles_n, sp.n_split, sp.nk_split, part,
+                       use_t16 ? t16->pairing : 0, use_t16 ? t16->head_dim : 0);
     if (int e = launch_status()) return e;
     if (deferred) {
       *deferred = sp.n_split;
@@ -785,12 +1016,16 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   const LinWsTile& t = kLinWsTiles[ti];
   const int tiles_n = static_cast<int>((N + t.bn - 1) / t.bn);
   const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
+  const bool use_t16 = ti == kSplitTile && t16_usable(t16, N, group, -1);
+  const LinWsFn fn = use_t16 ? lin_ws_t16_fn<0>() : kLinWsFns[ti];
   if (kLinWsLds[ti] > 64 * 1024) {
-    Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kLinWsFns[ti]),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLinWsLds[ti])));
+    Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(kLinWsLds[ti])));
   }
-  hipLaunchKernelGGL(kLinWsFns[ti], dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl, qw, sc, y, res,
-                     (int)M, (int)N, (int)K, group, tiles_n, 1, 0, nullptr);
+  hipLaunchKernelGGL(fn, dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), kLinWsLds[ti], st, xh, xl,
+                     use_t16 ? static_cast<const int32_t*>(t16->tiles) : qw, use_t16 ? t16->scales : sc, y, res, (int)M,
+                     (int)N, (int)K, group, tiles_n, 1, 0, nullptr, use_t16 ? t16->pairing : 0,
+                     use_t16 ? t16->head_dim : 0);
   return launch_status();
 }
 
@@ -798,7 +1033,8 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
 // M <= 256 (64x256, one workgroup per CU); other shapes return Q4_ERR_UNSUPPORTED and the caller runs
 // q4_linear_planes + silu_mul_planes. oh / ol: the [M, N / 2] output planes (must not alias xh / xl).
 int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
-                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st) {
+                            uint16_t* oh, uint16_t* ol, int64_t N, int64_t K, int group, hipStream_t st,
+                            const T16Src* t16) {
   if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
   if (!oh || !ol) return Q4_ERR_NULL;
   const char* ov = getenv("Q4_LINEAR_CFG");
@@ -806,7 +1042,8 @@ int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, c
   constexpr LinWsTile t = kLinWsTiles[kSplitTile];
   const int64_t wide = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (!(M <= 256 && wide >= 256) || N % t.bn || (N / 2) % 32 || ol != oh + M * (N / 2)) return Q4_ERR_UNSUPPORTED;
-  auto fn = q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, 1>;
+  const bool use_t16 = t16_usable(t16, N, group, Q4_PAIR_SWIGLU);
+  const LinWsFn fn = use_t16 ? lin_ws_t16_fn<1>() : q4_linear_ws_kernel<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks, 1, t.pipe>;
   constexpr size_t lds = LinWsCfg<t.bm, t.bn, t.wm, t.wn, t.nst, t.ks>::kLds;
   if (lds > 64 * 1024) {
     Q4_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -814,8 +1051,10 @@ int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, c
   }
   const int tiles_n = static_cast<int>(N / t.bn);
   const int tiles = static_cast<int>((M + t.bm - 1) / t.bm) * tiles_n;
-  hipLaunchKernelGGL(fn, dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), lds, st, xh, xl, qw, sc,
-                     reinterpret_cast<float*>(oh), nullptr, (int)M, (int)N, (int)K, group, tiles_n, 1, 0, nullptr);
+  hipLaunchKernelGGL(fn, dim3(tiles), dim3(64 * t.wm * t.wn * t.ks), lds, st, xh, xl,
+                     use_t16 ? static_cast<const int32_t*>(t16->tiles) : qw, use_t16 ? t16->scales : sc,
+                     reinterpret_cast<float*>(oh), nullptr, (int)M, (int)N, (int)K, group, tiles_n, 1, 0, nullptr,
+                     use_t16 ? t16->pairing : 0, use_t16 ? t16->head_dim : 0);
   return launch_status();
 }
 

@@ -195,6 +195,10 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   // decode GEMVs on the T16 copies where the model has them (Q4_NO_T16 set: the reference layout)
   const bool use_t16 = fused && !getenv("Q4_NO_T16");
   auto has = [&](const q4llm_t16& t) { return use_t16 && t.tiles && t.scales; };
+  // prefill projections on the 64x256 tile read the same T16 copies (fewer cache lines per load)
+  auto src = [&](const q4llm_t16& t, int pairing) {
+    return q4::T16Src{t.tiles, static_cast<const uint16_t*>(t.scales), pairing, hd};
+  };
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   // K-split partials left by the last prefill projection for the kernel after it to add (0: none)
   int pending = 0;
@@ -217,8 +221,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       // the qkv partials are added by the RoPE + KV-write kernel
       const bool defer_rope = q4::rope_kv_takes_partials(qkv, m->cos_t, m->sin_t, kc, vc, hd);
       int qkv_split = 0;
+      const q4::T16Src qkv_t = src(ly.wqkv_t, Q4_PAIR_ROPE);
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st, part,
-                                  lo.part_bytes, defer_rope ? &qkv_split : nullptr));
+                                  lo.part_bytes, defer_rope ? &qkv_split : nullptr, &qkv_t));
       if (qkv_split > 0)
         Q4_TRY(q4::rope_kv_partials(qkv, part, qkv_split, m->cos_t, m->sin_t, kc, vc, C, nh, nkv, hd, m->max_ctx, start,
                                     st));
@@ -233,8 +238,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       Q4_TRY(q4::attn_bucket_planes(qkv, qkv_w, kc, vc, xh, xl, C, nh, nkv, hd, L, start, scale, attn_ws,
                                     lo.attn_bytes, st));
       // the o-projection's partials are added to h by the post-attention norm
+      const q4::T16Src wo_t = src(ly.wo_t, Q4_PAIR_NONE);
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wo_q, ly.wo_s, h, h, D, nq_w, m->group, st, part, lo.part_bytes,
-                                  defer_norm ? &pending : nullptr));
+                                  defer_norm ? &pending : nullptr, &wo_t));
     } else {
       Q4_TRY(attn_bucket(qkv, qkv_w, kc, vc, o, C, nh, nkv, hd, L, start, scale, attn_ws, lo.attn_bytes, stream));
       if (has(ly.wo_t))
@@ -262,18 +268,20 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       // holds the [C, 2 inter] fp32 otherwise), else the GEMM and silu_mul as two kernels
       uint16_t* ah = reinterpret_cast<uint16_t*>(gu);
       uint16_t* al = ah + static_cast<int64_t>(C) * m->inter;
-      const int fused = q4::q4_linear_planes_swiglu(xh, xl, C, ly.wgu_q, ly.wgu_s, ah, al, 2 * m->inter, D, m->group, st);
+      const q4::T16Src wgu_t = src(ly.wgu_t, Q4_PAIR_SWIGLU), wdown_t = src(ly.wdown_t, Q4_PAIR_NONE);
+      const int fused =
+          q4::q4_linear_planes_swiglu(xh, xl, C, ly.wgu_q, ly.wgu_s, ah, al, 2 * m->inter, D, m->group, st, &wgu_t);
       // the down projection's partials are added to h by the next layer's input norm (or the final norm)
       if (fused == Q4_OK) {
         Q4_TRY(q4::q4_linear_planes(ah, al, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
-                                    lo.part_bytes, defer_norm ? &pending : nullptr));
+                                    lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));
       } else {
         if (fused != Q4_ERR_UNSUPPORTED) return fused;
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st, part,
                                     lo.part_bytes));
         Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
-                                    lo.part_bytes, defer_norm ? &pending : nullptr));
+                                    lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));
       }
     } else {
       Q4_TRY(rmsnorm_f32(h, ly.ln_post, x, C, D, m->eps, nullptr, stream));

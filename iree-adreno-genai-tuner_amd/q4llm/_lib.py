@@ -144,7 +144,7 @@ def config_table(kind: str):
     """Entries of one of the library's explicit tile lists as tuples (see include/q4llm.h):
     'gemv', 'gemv_mx', 'gemm' or 'linear_ws'."""
     fn, width = {"gemv": ("q4_gemv_config_info", 6), "gemv_mx": ("q4_gemv_mx_config_info", 5),
-                 "gemm": ("gemm_f16_config_info", 7), "linear_ws": ("q4_linear_ws_config_info", 6)}[kind]
+                 "gemm": ("gemm_f16_config_info", 7), "linear_ws": ("q4_linear_ws_config_info", 7)}[kind]
     out = []
     buf = (C.c_int * 8)()
     while LIB.raw(fn)(len(out), buf) == Q4_OK:

@@ -164,6 +164,33 @@ def test_prefill_chunk128_k_split_paths_vs_oracle(dev):
         assert (l_o.cpu() - r_l).abs().max().item() <= tol(r_l), s0
 
 
+@pytest.mark.parametrize("chunk", [256, 128])
+def test_prefill_t16_source_matches_reference_layout(dev, monkeypatch, chunk):
+    """Prefill projections on the 64x256 tile read the decode T16 copies (RoPE-paired qkv, plain o and
+    down, SwiGLU-paired gate/up) instead of the reference layout: the same sums in the same order, so
+    the logits and the K/V caches are bit-identical to Q4_PREFILL_REF_LAYOUT (256-row chunk: the SwiGLU
+    epilogue; 128 rows: every projection K-split), and the token matches the oracle."""
+    cfg = dict(synth.TINY, hidden_size=1024, num_attention_heads=8, num_key_value_heads=4, head_dim=128,
+               intermediate_size=8192, num_hidden_layers=2)
+    ours, ref = build_pair(cfg, 128, 256)
+    assert all((i, nm) in ours.t16 for i in range(2) for nm in ("wqkv", "wo", "wgu", "wdown"))
+    prompt = synth.prompt_ids(256, cfg["vocab_size"], seed=11)
+    toks = torch.tensor([prompt[:chunk]], dtype=torch.int32)
+    start, last = torch.tensor([0], dtype=torch.int32), torch.tensor([chunk - 1], dtype=torch.int32)
+    c_t = ours.new_caches()
+    n_t, l_t = ours.step(toks, start, last, c_t, 256)
+    monkeypatch.setenv("Q4_PREFILL_REF_LAYOUT", "1")
+    c_r = ours.new_caches()
+    n_r, l_r = ours.step(toks, start, last, c_r, 256)
+    monkeypatch.delenv("Q4_PREFILL_REF_LAYOUT")
+    assert torch.equal(l_t, l_r) and int(n_t.item()) == int(n_r.item())
+    for a, b in zip(c_t, c_r):
+        assert torch.equal(a, b)
+    r_n, r_l = ref.step(toks, start, last, ref.new_caches(), 256)
+    assert int(n_t.item()) == int(r_n.item())
+    assert (l_t.cpu() - r_l).abs().max().item() <= tol(r_l)
+
+
 def test_group16_step_and_generation_vs_oracle(dev):
     """group 16 (legal in the reference: group % 8 == 0, llama_q4.py:31): the matrix-core prefill GEMM
     takes only groups of 32 * 2^j, so prefill runs one GEMV per row; decode takes the generic GEMV

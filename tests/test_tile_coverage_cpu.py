@@ -382,7 +382,7 @@ def test_gemm_split_rule_fills_the_cus():
 # ------------------------------------------------------------------------------------------------
 
 def replay_linear_ws(cfg, M, N, K, group):
-    bm, bn, wm, wn, nst, ks_n = cfg
+    bm, bn, wm, wn, nst, ks_n, pipe = cfg
     waves = wm * wn * ks_n
     kai = cdiv(bm // 8, waves)
     kbi = cdiv(bn // 32, waves)
@@ -475,3 +475,121 @@ def test_gemm_swizzle_is_bank_conflict_free(bk):
     # and the identity mapping (no swizzle) would not be: the check discriminates
     groups = {((r * row_b) // 16) % 16 for r in range(16)}
     assert len(groups) < 16
+
+
+# ------------------------------------------------------------------------------------------------
+# W4A16 prefill GEMM reading the decode T16 copy (csrc/q4_linear.hip: q4_linear_ws_kernel, T16 = true;
+# layout: csrc/q4_t16.hip t16_pack_weights / t16_pack_scales / t16_row)
+# ------------------------------------------------------------------------------------------------
+
+def t16_row(vr, N, pairing, hd):
+    """Weight row of T16 virtual row vr (-1: padding); pairing 0 none, 1 SwiGLU, 2 RoPE."""
+    if pairing == 0:
+        return vr if vr < N else -1
+    v = vr & 15
+    p = (vr >> 4) * 8 + (v & 7)
+    if p >= N // 2:
+        return -1
+    if pairing == 1:
+        return p + (N // 2 if v >= 8 else 0)
+    hh = hd // 2
+    head, d = divmod(p, hh)
+    return head * hd + d + (hh if v >= 8 else 0)
+
+
+def t16_pack(qbytes, sc, N, K, group, pairing, hd):
+    """Byte image of the T16 tiles and the fp16 scale array, restated from q4_t16.hip."""
+    tile_k = 4 * group
+    n_tiles = cdiv(K, tile_k)
+    nseg = n_tiles * tile_k // 128
+    n_t16 = cdiv(N, 16) if pairing == 0 else cdiv(N // 2, 8)
+    tiles = np.zeros((n_t16, nseg, 16, 64), np.uint8)
+    scales = np.zeros((n_t16, n_tiles, 4, 16), np.uint16)
+    kg = K // group
+    for t in range(n_t16):
+        for v in range(16):
+            row = t16_row(16 * t + v, N, pairing, hd)
+            if row < 0:
+                continue
+            for seg in range(nseg):
+                k0 = seg * 128
+                if k0 < K:
+                    tiles[t, seg, v] = qbytes[row, k0 // 2:k0 // 2 + 64]
+            for T in range(n_tiles):
+                for q in range(4):
+                    if 4 * T + q < kg:
+                        scales[t, T, q, v] = sc[row, 4 * T + q]
+    return tiles.reshape(-1), scales.reshape(-1), n_t16, n_tiles, nseg
+
+
+@pytest.mark.parametrize("pairing,N,K,group", [(0, 200, 1024, 128), (2, 256 + 64, 768, 128), (1, 512 + 32, 512, 32),
+                                               (0, 96, 1536, 32)])
+def test_linear_ws_t16_loads_and_outputs(pairing, N, K, group):
+    """Every 1 KB weight load of a 64-k stage of 32 virtual columns brings, for LDS row r (lane / 2), the
+    64 nibbles of weight row t16_row(column) at that stage; every scale slot holds the fp16 scale of that
+    row and the stage's group; and the epilogue writes each virtual column to t16_row (RoPE, none) or,
+    for SwiGLU, each pair once from the lane holding gate with up 8 columns away."""
+    hd = 64
+    cfg = config_table("linear_ws")[-1]
+    bm, bn, wm, wn, nst, ks_n, pipe = cfg
+    assert bn % 128 == 0 and ks_n == 1 and pipe == 1
+    waves = wm * wn
+    rng = np.random.default_rng(N + K)
+    qbytes = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    sc = rng.integers(0, 0x7BFF, size=(N, K // group), dtype=np.uint16)
+    tiles, scales, n_t16, n_tiles, nseg = t16_pack(qbytes, sc, N, K, group, pairing, hd)
+    lane = np.arange(64)
+    gshift = group.bit_length() - 1
+    for n0 in range(0, cdiv(N, bn) * bn, bn):
+        for kt in range(K // 64):
+            k0 = 64 * kt
+            # weights: instruction j of wave w fills virtual rows 32 b .. 32 b + 31, b = w + j waves
+            for b in range(bn // 32):
+                t = (n0 + 32 * b) // 16 + (lane >> 5)
+                off = t * nseg * 1024 + ((lane & 31) >> 1) * 64 + (lane & 1) * 16 + (kt >> 1) * 1024 + (kt & 1) * 32
+                for ln in range(64):
+                    vc = n0 + 32 * b + ln // 2
+                    got = tiles[off[ln]:off[ln] + 16] if t[ln] < n_t16 else np.zeros(16, np.uint8)
+                    row = t16_row(vc, N, pairing, hd) if vc < 16 * n_t16 else -1
+                    want = qbytes[row, k0 // 2 + 16 * (ln & 1): k0 // 2 + 16 * (ln & 1) + 16] if row >= 0 else 0
+                    assert (got == want).all(), (n0, kt, b, ln)
+            # scales: instruction i (< 2 bn / 128) fills slot i // (bn / 128), part i % (bn / 128)
+            parts = bn // 128
+            for i in range(2 * parts):
+                slot, part = divmod(i, parts)
+                g = (k0 >> gshift) if slot == 0 else ((k0 + 63) >> gshift)
+                t = n0 // 16 + part * 8 + (lane >> 3)
+                e = ((t * n_tiles + (g >> 2)) * 4 + (g & 3)) * 16 + 2 * (lane & 7)
+                for ln in range(64):
+                    for h in range(2):
+                        col = part * 128 + 2 * ln + h  # virtual column of the fp16 in LDS
+                        vc = n0 + col
+                        row = t16_row(vc, N, pairing, hd) if vc < 16 * n_t16 else -1
+                        got = scales[e[ln] + h] if t[ln] < n_t16 else 0
+                        assert got == (sc[row, g] if row >= 0 else 0), (n0, kt, i, ln, h)
+        assert waves * 1 >= 2 * (bn // 128)  # one scale instruction per wave covers both slots
+    # epilogue column mapping (q4_linear_ws_kernel: the T16 branches of the EPI 0 / EPI 1 stores)
+    cols = np.arange(16 * n_t16)
+    if pairing == 1:
+        seen = np.zeros(N // 2, np.int32)
+        for vc in cols:
+            if vc & 8:
+                continue
+            pr = 8 * (vc >> 4) + (vc & 7)
+            if pr < N // 2:
+                assert t16_row(vc, N, 1, hd) == pr and t16_row(vc + 8, N, 1, hd) == pr + N // 2
+                seen[pr] += 1
+        assert (seen == 1).all()
+    else:
+        seen = np.zeros(N, np.int32)
+        for vc in cols:
+            col = vc
+            if pairing == 2:
+                pr, hh = 8 * (vc >> 4) + (vc & 7), hd >> 1
+                sh = hh.bit_length() - 1
+                head = pr >> sh
+                col = head * hd + (pr - (head << sh)) + (hh if vc & 8 else 0) if pr < N // 2 else N
+            if col < N:
+                assert col == t16_row(vc, N, pairing, hd)
+                seen[col] += 1
+        assert (seen == 1).all()
