@@ -645,7 +645,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     // The MFMAs of 16-k step q from fragment set `set` (x_hi products of every tile, then x_lo, so
     // consecutive MFMAs write different tiles), with loads [q kLPW / 3, (q + 1) kLPW / 3) of K step
     // kt_begin + ld (q < 3) placed one after each of the first MFMAs.
-    auto mfma_sub = [&](int set, int q, int ld) {
+    auto mfma_sub = [&](int set, int q, int ld, auto zero) {
       half8 fb[G::TN];
 #pragma unroll
       for (int j = 0; j < G::TN; ++j) fb[j] = nibbles_to_half8(fw[set][j], mg);
@@ -653,7 +653,8 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
       for (int i = 0; i < G::TM; ++i)
 #pragma unroll
         for (int j = 0; j < G::TN; ++j)
-          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[set][i], fb[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[set][i], fb[j], decltype(zero)::value ? float16v{} : part[i][j],
+                                                             0, 0, 0);
 #pragma unroll
       for (int i = 0; i < G::TM; ++i)
 #pragma unroll
@@ -698,16 +699,23 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     read_sub(0, 0, 0);
-    for (int l = 0; l < nl; ++l) {
+    // One K step; par = 0 / 1: its parity inside a group of 128 (two steps; K splits cut whole groups,
+    // so kt_begin is even): the group's first MFMAs take a zero accumulator and its scale is applied
+    // once after the last MFMAs of the odd step, with no zeroing and no branch. par = -1: any group,
+    // checked after every 16-k step.
+    using no = std::false_type;
+    auto step_body = [&](int l, auto par) {
+      constexpr int kPar = decltype(par)::value;
       const int ld = l + NST - 1;
 #pragma unroll
       for (int kk = 0; kk < KK - 1; ++kk) {
         read_sub(l, kk + 1, (kk + 1) & 1);
-        if (kk == 0) read_scales(l);
+        if (kk == 0 && kPar != 0) read_scales(l);
         __builtin_amdgcn_sched_barrier(0);
-        mfma_sub(kk & 1, kk, ld);
+        if (kPar == 0 && kk == 0) mfma_sub(0, 0, ld, std::true_type{});
+        else mfma_sub(kk & 1, kk, ld, no{});
         __builtin_amdgcn_sched_barrier(0);
-        scale_end(l, kk);
+        if constexpr (kPar < 0) scale_end(l, kk);
       }
       if (l + 1 < nl) {
         // this wave's loads of step l + 1 landed (steps up to l + NST - 1 issued); its reads of step l
@@ -720,9 +728,29 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
         read_sub(l + 1, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      mfma_sub(1, KK - 1, -1);
+      mfma_sub(1, KK - 1, -1, no{});
       __builtin_amdgcn_sched_barrier(0);
-      scale_end(l, KK - 1);
+      if constexpr (kPar < 0) {
+        scale_end(l, KK - 1);
+      } else if constexpr (kPar == 1) {
+        const int g = ((kt_begin + l) * 64) >> gshift;
+#pragma unroll
+        for (int j = 0; j < G::TN; ++j) {
+          const float sc = half_bits_to_float(static_cast<uint16_t>(T16 ? sw0[j] : sw0[j] >> (16 * (scale_elem(j, g) & 1))));
+#pragma unroll
+          for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(part[i][j][e], sc, acc[i][j][e]);
+        }
+      }
+    };
+    if (group == 128) {
+      for (int l = 0; l < nl; l += 2) {
+        step_body(l, std::integral_constant<int, 0>{});
+        step_body(l + 1, std::integral_constant<int, 1>{});
+      }
+    } else {
+      for (int l = 0; l < nl; ++l) step_body(l, std::integral_constant<int, -1>{});
     }
     wait_vmcnt<0>();  // the last steps' (zero) loads have landed before the waves exit
   }
@@ -758,24 +786,30 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
   }
 
   if constexpr (EPI == 1 && T16) {
-    // virtual column c of a 16-column group: gate row 8 (c / 16) + c % 8 for c % 16 < 8, its up row 8
-    // columns later; lane l (column l % 32) swaps with lane l ^ 8 (DPP row rotate by 8)
+    // Virtual column c of a 16-column group: gate row 8 (c / 16) + c % 8 for c % 16 < 8, its up row 8
+    // columns later. Tiles j and j + 1 are paired so that every lane finishes one pair: lanes with
+    // c % 16 < 8 keep gate of tile j and receive its up from lane l ^ 8, lanes with c % 16 >= 8 keep up
+    // of tile j + 1 and receive its gate (one DPP row rotate by 8 per two outputs).
+    static_assert(G::TN % 2 == 0, "tiles are paired");
     const int I = N >> 1;
     uint16_t* oh = reinterpret_cast<uint16_t*>(Y);
     uint16_t* ol = oh + static_cast<int64_t>(M) * I;
+    const bool hi8 = (lane & 8) != 0;
 #pragma unroll
     for (int i = 0; i < G::TM; ++i)
 #pragma unroll
-      for (int j = 0; j < G::TN; ++j)
+      for (int j = 0; j < G::TN; j += 2)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float g = acc[i][j][e];
-          const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, g), 0x128, 0xF, 0xF, false));
+          const float keep = hi8 ? acc[i][j + 1][e] : acc[i][j][e];
+          const float send = hi8 ? acc[i][j][e] : acc[i][j + 1][e];
+          const float got =
+              __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0x128, 0xF, 0xF, false));
+          const float g = hi8 ? got : keep, u = hi8 ? keep : got;
           const int row = m0 + wm * G::WTM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-          const int vc = n0 + wn * G::WTN + j * 32 + (lane & 31);
+          const int vc = n0 + wn * G::WTN + (j + (hi8 ? 1 : 0)) * 32 + (lane & 31);
           const int pr = 8 * (vc >> 4) + (vc & 7);
-          if ((lane & 8) == 0 && row < M && pr < I)
-            store_x_planes(oh, ol, static_cast<int64_t>(row) * I + pr, silu_mul_exact(g, u));
+          if (row < M && pr < I) store_x_planes(oh, ol, static_cast<int64_t>(row) * I + pr, silu_mul_exact(g, u));
         }
     return;
   } else if constexpr (EPI == 1) {

@@ -571,14 +571,19 @@ def test_linear_ws_t16_loads_and_outputs(pairing, N, K, group):
     # epilogue column mapping (q4_linear_ws_kernel: the T16 branches of the EPI 0 / EPI 1 stores)
     cols = np.arange(16 * n_t16)
     if pairing == 1:
+        # tiles j, j + 1 (32 columns each) paired: lane l with l % 16 < 8 takes gate column c of tile j
+        # and its up at c + 8 (from lane l ^ 8); lane l with l % 16 >= 8 takes up column c of tile j + 1
+        # and its gate at c - 8; both write pair 8 (c / 16) + c % 8
         seen = np.zeros(N // 2, np.int32)
-        for vc in cols:
-            if vc & 8:
-                continue
-            pr = 8 * (vc >> 4) + (vc & 7)
-            if pr < N // 2:
-                assert t16_row(vc, N, 1, hd) == pr and t16_row(vc + 8, N, 1, hd) == pr + N // 2
-                seen[pr] += 1
+        for base in range(0, 16 * n_t16, 64):
+            for ln in range(32):
+                hi8 = (ln & 8) != 0
+                vc = base + (32 if hi8 else 0) + ln
+                gate_c, up_c = (vc - 8, vc) if hi8 else (vc, vc + 8)
+                pr = 8 * (vc >> 4) + (vc & 7)
+                if vc < 16 * n_t16 and pr < N // 2:
+                    assert t16_row(gate_c, N, 1, hd) == pr and t16_row(up_c, N, 1, hd) == pr + N // 2
+                    seen[pr] += 1
         assert (seen == 1).all()
     else:
         seen = np.zeros(N, np.int32)
