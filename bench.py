@@ -355,6 +355,56 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5, vendor=False):
     return out
 
 
+W4A16_SHAPES = [(256, 5120, 3072), (256, 3072, 3072), (256, 16384, 3072), (256, 3072, 8192)]
+
+
+def bench_w4a16(dev, reps=5):
+    """The 3B prefill projections of a 256-row chunk (qkv, o, gate/up, down; group 128) through the C-ABI
+    q4_linear_ws on the reference weight layout: x split into fp16 planes, the GEMM (K split over the
+    workspace where the rule takes one) and the partial reduce, all in the timed launch sequence, over
+    rotated weight copies. Parity and the CPU figure: the reference QLinear on the host (per-call
+    dequant + fp32 F.linear, llama_q4.py:72) over the same x and weights; error is max|y - ref| /
+    rms(ref). The model's own step runs the same GEMM on the T16 copies with the partials added by the
+    next kernel (profiles/decode_3b_step_kernel_stats.md)."""
+    import torch
+    from oracle import llama_q4_ref as R
+    from q4llm import ops
+    cores = cpu_threads()
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    for (M, N, K) in W4A16_SHAPES:
+        w = torch.randn(N, K, generator=g) * 0.02
+        qw, sc = R.quantize_q4(w, 128)
+        x = torch.randn(M, K, generator=g)
+        wbytes = N * K // 2 + N * (K // 128) * 2
+        nb = max(4, -(-2 * MALL_BYTES // wbytes))
+        copies = [(qw.to(dev), sc.to(dev)) for _ in range(nb)]
+        xd = x.to(dev)
+        y = torch.empty(M, N, device=dev)
+        ws = torch.empty(ops.q4_linear_ws_split_bytes(M, N, K, 128), dtype=torch.uint8, device=dev)
+        ops.q4_linear_ws(xd, copies[0][0], copies[0][1], 128, out=y, workspace=ws)
+        got = y.cpu()
+        box = {}
+
+        def host_ref():
+            box["r"] = torch.nn.functional.linear(x, R.dequantize_q4(qw, sc, 128))
+
+        cpu_ms, cpu_n = cpu_time_ms(host_ref, reps=3, budget_s=6.0)
+        ref = box["r"]
+        err = (got - ref).abs().max().item() / ref.pow(2).mean().sqrt().item()
+        fns = [lambda q=q, s_=s_: ops.q4_linear_ws(xd, q, s_, 128, out=y, workspace=ws) for q, s_ in copies]
+        st = stats_us(timed_steps(fns, max(16, 2 * len(fns)), len(fns), reps))
+        flops = 2.0 * M * N * K
+        out[f"{M}x{N}x{K}"] = {"us": st["median"], "us_min": st["min"], "reps": st["reps"],
+                               "TFLOP/s": round(flops / st["median"] / 1e6, 1), "err_over_rms": float(f"{err:.3e}"),
+                               "cpu_ms": round(cpu_ms, 3), "cpu_cores": cores, "cpu_reps": cpu_n}
+        log(f"w4a16 {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}); host QLinear {cpu_ms:.1f} ms; "
+            f"err/rms {err:.2e}")
+        del copies, xd, y, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_attn(dev, reps=5):
     """Config 4 (24/8 heads, hd 128, one query row at position valid - 1). CPU figure: the oracle's
     attention block (llama_q4.py:224-232) over the same caches on this host's cores."""
@@ -531,6 +581,7 @@ def main():
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="also time torch.matmul (hipBLASLt) on the GEMM shapes, for comparison")
     ap.add_argument("--skip-attn", action="store_true")
+    ap.add_argument("--skip-w4a16", action="store_true", help="leave out the prefill W4A16 GEMM leg")
     ap.add_argument("--skip-gemv", action="store_true",
                     help="leave out the GEMV and probe legs (profiling the other legs; the line then has no value)")
     ap.add_argument("--skip-native", action="store_true",
@@ -567,6 +618,8 @@ def main():
                                          vendor=a.vendor_gemm)
         if not a.skip_attn:
             out["attn_decode"] = bench_attn(dev)
+        if not a.skip_w4a16:
+            out["w4a16_prefill"] = bench_w4a16(dev)
         if not a.skip_e2e:
             out["e2e_3b"] = bench_e2e(dev, native=not a.skip_native, cpu=not a.skip_cpu)[0]
         print(json.dumps(out), flush=True)
@@ -638,6 +691,8 @@ def main():
         out["gemm_f16"] = bench_gemm(dev, shapes, vendor=a.vendor_gemm)
     if not a.skip_attn:
         out["attn_decode"] = bench_attn(dev)
+    if not a.skip_w4a16:
+        out["w4a16_prefill"] = bench_w4a16(dev)
     if not a.skip_e2e:
         e2e, tokens = bench_e2e(dev, native=not a.skip_native, cpu=not a.skip_cpu)
         out["e2e_3b"] = e2e
