@@ -258,6 +258,82 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
   }
 }
 
+// Merge the splits of each (row, head), one thread per 8 dims of one (row, head): no LDS and no
+// barrier. Every (m, l) and this thread's 8 o values of the first kB splits are requested before
+// the position is read (range-checked buffer loads: zeros past the workspace), so the merge costs one
+// memory round trip; splits past the position are masked by selection (their workspace entries may
+// hold anything). M, the denominator and the numerator run over the splits in ascending order.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine8_kernel(const float* __restrict__ ws_ml, const float* __restrict__ ws_o,
+                                                          float* __restrict__ out, int64_t rows, int n_q, int n_splits,
+                                                          int S, const int32_t* __restrict__ start_p,
+                                                          uint16_t* __restrict__ xh, uint16_t* __restrict__ xl) {
+  constexpr int kB = 8, D8 = HD / 8;
+  typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= rows * D8) return;
+  const int64_t ch = t / D8;  // (row, head) = c * n_q + h
+  const int d8 = static_cast<int>(t - ch * D8);
+  const int c = static_cast<int>(ch / n_q);
+  const uint32_t n_ent = static_cast<uint32_t>(rows) * n_splits;
+  const __amdgpu_buffer_rsrc_t mr = make_rsrc(ws_ml, n_ent * 8u);
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(ws_o, n_ent * HD * 4u);
+  const uint32_t e0 = static_cast<uint32_t>(ch) * n_splits;
+  f32x2 ml[kB];
+  f32x4 oa[kB], ob[kB];
+#pragma unroll
+  for (int j = 0; j < kB; ++j) {
+    const bool in = j < n_splits;
+    ml[j] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(mr, in ? (e0 + j) * 8u : 0x80000000u, 0, 0));
+    const uint32_t oo = in ? ((e0 + j) * HD + 8 * d8) * 4u : 0x80000000u;
+    oa[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(orr, oo, 0, 0));
+    ob[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(orr, oo + 16u, 0, 0));
+  }
+  const int pos = start_p[0] + c;
+  const int ns = min(n_splits, pos / S + 1);
+  float M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kB; ++j)
+    if (j < ns) M = fmaxf(M, ml[j].x);
+  for (int j = kB; j < ns; ++j) M = fmaxf(M, ws_ml[2 * (static_cast<size_t>(e0) + j)]);
+  float den = 0.0f, num[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) num[e] = 0.0f;
+  auto add = [&](float m, float l, const f32x4& a, const f32x4& b) {
+    const float w = m == -INFINITY ? 0.0f : expf(m - M);
+    den = fmaf(w, l, den);
+    num[0] = fmaf(w, a.x, num[0]);
+    num[1] = fmaf(w, a.y, num[1]);
+    num[2] = fmaf(w, a.z, num[2]);
+    num[3] = fmaf(w, a.w, num[3]);
+    num[4] = fmaf(w, b.x, num[4]);
+    num[5] = fmaf(w, b.y, num[5]);
+    num[6] = fmaf(w, b.z, num[6]);
+    num[7] = fmaf(w, b.w, num[7]);
+  };
+#pragma unroll
+  for (int j = 0; j < kB; ++j)
+    if (j < ns) add(ml[j].x, ml[j].y, oa[j], ob[j]);
+  for (int j = kB; j < ns; ++j) {
+    const size_t e = static_cast<size_t>(e0) + j;
+    const float4* op = reinterpret_cast<const float4*>(ws_o + e * HD + 8 * d8);
+    const float4 a = op[0], b = op[1];
+    add(ws_ml[2 * e], ws_ml[2 * e + 1], f32x4{a.x, a.y, a.z, a.w}, f32x4{b.x, b.y, b.z, b.w});
+  }
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = num[e] / den;
+  if (xh) {
+    store_x_planes8(xh, xl, ch * D8 + d8, v);  // the o-projection's x planes
+  } else {
+    float4* dst = reinterpret_cast<float4*>(out + ch * HD + 8 * d8);
+    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 // Merge the splits of each (row, head): o = sum_i e^(m_i - M) o_i / sum_i e^(m_i - M) l_i.
 // One workgroup of HD threads per (row, head); only the splits holding keys <= pos are used. The loads
 // that do not need the position are issued first: this thread's dim of the first kBatch splits' o
@@ -911,6 +987,18 @@ int attn_bucket_impl(const float* q, int q_row_stride, const uint16_t* k_cache, 
     else rc = launch_split<64, 128>(p, q, q_row_stride, k_cache, v_cache, ws_ml, ws_o, C, n_q, n_kv, L, start, scale, st);
   }
   if (rc) return rc;
+  const int64_t rows = static_cast<int64_t>(C) * n_q;
+  if (rows * p.n_splits * hd * 4 < (int64_t{1} << 31) && (!xh || (aligned(xh, 16) && aligned(xl, 16))) &&
+      (xh || aligned(out, 16)) && !getenv("Q4_ATTN_COMBINE_WG")) {
+    const unsigned blocks = static_cast<unsigned>((rows * (hd / 8) + 255) / 256);
+    if (hd == 128)
+      hipLaunchKernelGGL(attn_combine8_kernel<128>, dim3(blocks), dim3(256), 0, st, ws_ml, ws_o, out, rows, n_q,
+                         p.n_splits, p.S, start, xh, xl);
+    else
+      hipLaunchKernelGGL(attn_combine8_kernel<64>, dim3(blocks), dim3(256), 0, st, ws_ml, ws_o, out, rows, n_q,
+                         p.n_splits, p.S, start, xh, xl);
+    return launch_status();
+  }
   if (hd == 128)
     hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(C * n_q), dim3(128), 0, st, ws_ml, ws_o, out, n_q, p.n_splits,
                        p.S, start, xh, xl);

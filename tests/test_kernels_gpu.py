@@ -95,15 +95,20 @@ def test_attn_decode_group_sizes(dev, monkeypatch, nq, nkv, hd, L, start, path):
 @pytest.mark.parametrize("Cn,start,L,nq,nkv,hd", [(256, 0, 256, 24, 8, 128), (256, 256, 512, 24, 8, 128),
                                                   (16, 0, 64, 4, 2, 64), (8, 13, 32, 8, 2, 32 * 2), (5, 3, 64, 4, 2, 64),
                                                   (100, 37, 200, 8, 8, 128), (70, 500, 600, 16, 2, 128),
-                                                  (128, 128, 384, 32, 8, 64), (33, 0, 40, 40, 8, 128)])
-@pytest.mark.parametrize("path", ["mfma", "generic"])
+                                                  (128, 128, 384, 32, 8, 64), (33, 0, 40, 40, 8, 128),
+                                                  (48, 1900, 2048, 24, 8, 128)])
+@pytest.mark.parametrize("path", ["mfma", "generic", "mfma_wg_combine"])
 def test_attn_prefill_chunk(dev, monkeypatch, Cn, start, L, nq, nkv, hd, path):
     """Prefill chunks on the matrix-core kernel (group sizes 1-8) and on the generic split kernel
-    (forced; also the path for group sizes above 8): ragged C and L, start > 0."""
+    (forced; also the path for group sizes above 8): ragged C and L, start > 0, up to 16 key splits
+    (past the 8 the combine loads up front); the splits merged by the per-thread combine kernel or
+    (Q4_ATTN_COMBINE_WG) by the workgroup-per-(row, head) one."""
+    monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
+    monkeypatch.delenv("Q4_ATTN_COMBINE_WG", raising=False)
     if path == "generic":
         monkeypatch.setenv("Q4_ATTN_GENERIC", "1")
-    else:
-        monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
+    elif path == "mfma_wg_combine":
+        monkeypatch.setenv("Q4_ATTN_COMBINE_WG", "1")
     g = torch.Generator().manual_seed(Cn + start)
     qkv_w = (nq + 2 * nkv) * hd
     qkv = torch.randn(Cn, qkv_w, generator=g)
