@@ -720,9 +720,9 @@ int launch_decode(const AttnPlan& p, int hd, int g, const float* q, const uint16
 // permutation (lane half h supplies keys 16u + 8(i/4) + 4h + i%4) and V^T is read from LDS in the
 // same order, so no transpose of P is needed. O^T's column is the lane's query, so the softmax
 // rescale is per lane. The partial (m, l, o) of each (row, head, split) goes to the workspace and
-// attn_combine_kernel merges the splits. The next key block's K/V rows are loaded into registers
-// while the current block is computed; the workgroup has at least 4 waves for that staging (waves
-// past the group size only stage).
+// attn_combine8_kernel merges the splits. Each key block's K/V rows are loaded into registers two
+// blocks ahead (two register sets) while the blocks before it are computed; the workgroup has at
+// least 4 waves for that staging (waves past the group size only stage).
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
@@ -785,8 +785,9 @@ __global__ __launch_bounds__(64 * kMfmaMaxG) void attn_prefill_mfma_kernel(
   const __amdgpu_buffer_rsrc_t vres = make_rsrc(vc, cache_bytes);
   // K/V rows of a 32-key block: chunk ch = threadIdx.x + i * nthr (row ch / KCH, 16-byte chunk ch % KCH);
   // keys past L read out of range (zeros).
-  uint4 kpre[kMaxCh], vpre[kMaxCh];
-  auto load_block = [&](int kb) {
+  // Two register sets: block kb's rows are requested two blocks ahead of their use.
+  uint4 kpa[kMaxCh], vpa[kMaxCh], kpb[kMaxCh], vpb[kMaxCh];
+  auto load_block = [&](int kb, uint4 (&kpre)[kMaxCh], uint4 (&vpre)[kMaxCh]) {
 #pragma unroll
     for (int i = 0; i < kMaxCh; ++i) {
       const int ch = threadIdx.x + i * nthr;
@@ -797,7 +798,7 @@ __global__ __launch_bounds__(64 * kMfmaMaxG) void attn_prefill_mfma_kernel(
       vpre[i] = buf_load16(vres, off);
     }
   };
-  auto stage_block = [&]() {
+  auto stage_block = [&](const uint4 (&kpre)[kMaxCh], const uint4 (&vpre)[kMaxCh]) {
 #pragma unroll
     for (int i = 0; i < kMaxCh; ++i) {
       const int ch = threadIdx.x + i * nthr;
@@ -820,11 +821,10 @@ __global__ __launch_bounds__(64 * kMfmaMaxG) void attn_prefill_mfma_kernel(
     for (int e = 0; e < 16; ++e) o[tt][e] = 0.0f;
   float m = -INFINITY, l = 0.0f;
 
-  load_block(k0);
-  for (int kb = k0; kb < k_end; kb += 32) {
-    stage_block();
+  auto block = [&](int kb, uint4 (&kpre)[kMaxCh], uint4 (&vpre)[kMaxCh]) {
+    stage_block(kpre, vpre);
     __syncthreads();
-    if (kb + 32 < k_end) load_block(kb + 32);  // in flight during this block's MFMAs
+    if (kb + 64 < k_end) load_block(kb + 64, kpre, vpre);  // in flight during the next two blocks
 
     // S^T = K Q^T: 32 keys (rows) x 32 queries (columns)
     float16v sacc;
@@ -884,6 +884,12 @@ __global__ __launch_bounds__(64 * kMfmaMaxG) void attn_prefill_mfma_kernel(
       }
     }
     __syncthreads();  // every wave is done with this block's K and V^T
+  };
+  load_block(k0, kpa, vpa);
+  if (k0 + 32 < k_end) load_block(k0 + 32, kpb, vpb);
+  for (int kb = k0; kb < k_end; kb += 64) {
+    block(kb, kpa, vpa);
+    if (kb + 32 < k_end) block(kb + 32, kpb, vpb);
   }
 
   if (row_ok) {
