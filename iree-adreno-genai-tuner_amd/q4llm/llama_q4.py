@@ -371,12 +371,18 @@ class LlamaQ4(nn.Module):
         self._raw_step(tok, tok.numel(), st, la, self._cache_ptrs(caches), L, nxt, logits)
         return nxt, logits
 
-    def entry_point(self, Cn, L, caches, logits=False):
+    def entry_point(self, Cn, L, caches, logits=False, steps=1):
         """Graph-backed entry point prefill_c{C}_l{L} / decode_l{L} (/ decode_logits_l{L}) bound to
-        `caches`: returns fn(tokens, start, last) -> next [1] int32 device tensor (or logits)."""
-        key = (Cn, L, logits, tuple(c.data_ptr() for c in caches))
+        `caches`: returns fn(tokens, start, last) -> next [1] int32 device tensor (or logits). With
+        steps > 1 (decode only): `steps` consecutive decode steps in one graph (_DecodeRun)."""
+        key = (Cn, L, logits, steps, tuple(c.data_ptr() for c in caches))
         if key not in self._graphs:
-            self._graphs[key] = _StepGraph(self, Cn, L, caches, logits)
+            if steps > 1:
+                if Cn != 1 or logits:
+                    raise ValueError("a multi-step entry point decodes one token per step and returns tokens")
+                self._graphs[key] = _DecodeRun(self, L, caches, steps)
+            else:
+                self._graphs[key] = _StepGraph(self, Cn, L, caches, logits)
         return self._graphs[key]
 
 
@@ -424,6 +430,11 @@ class _StepGraph:
         self.start.fill_(int(start))
         self.last.fill_(int(last))
 
+    def set_fed(self, start, token):
+        """Decode inputs for the next replay: position `start`, previous token `token`."""
+        self.start.fill_(int(start))
+        self.tokens.fill_(int(token))
+
     def replay(self):
         self.graph.replay()
         return self.logits if self.logits is not None else self.next
@@ -431,6 +442,53 @@ class _StepGraph:
     def __call__(self, tokens, start, last):
         self.set_inputs(tokens, start, last)
         return self.replay()
+
+
+class _DecodeRun:
+    """`steps` consecutive decode steps (C = 1, bucket L) captured into one HIP graph, so the host
+    launches and reads back once per `steps` tokens. The tokens sit in a ring of `steps` slots: step i
+    reads the token in slot i - 1 (step 0: the last slot, the previous replay's last token) and writes
+    its next token into slot i; every step is q4llm_step_feed, so a replay ends with start advanced
+    by `steps` and the device inputs already set for the next replay (`feeds_back`). replay() returns
+    the ring: the replay's `steps` tokens in order. Each step is the same q4llm_step as a one-step
+    decode graph, so the tokens are the ones `steps` one-step replays would give."""
+
+    def __init__(self, model: LlamaQ4, L, caches, steps):
+        dev = model.device
+        self.model, self.C, self.L, self.steps = model, 1, L, steps
+        self.feeds_back = True
+        self.start = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.last = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.ring = torch.zeros(steps, dtype=torch.int32, device=dev)
+        self.cache_arr = model._cache_ptrs(caches)
+        self.caches = caches
+        model.workspace(1, L)  # allocate before capture
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        # set-up launch outside capture at position max_ctx (no cache row written), as _StepGraph
+        self.start.fill_(model.max_ctx)
+        with torch.cuda.stream(s):
+            model._raw_step(self.ring[steps - 1:], 1, self.start, self.last, self.cache_arr, L, self.ring[:1], None)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        self.start.zero_()
+        self.ring.zero_()
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=s):
+            for i in range(steps):
+                j = (i - 1) % steps
+                model._raw_step(self.ring[j:j + 1], 1, self.start, self.last, self.cache_arr, L, self.ring[i:i + 1],
+                                None, feed=True)
+
+    def set_fed(self, start, token):
+        """Inputs for the next replay: position `start`, previous token `token` (in the last slot)."""
+        self.start.fill_(int(start))
+        self.ring[self.steps - 1:].fill_(int(token))
+
+    def replay(self):
+        self.graph.replay()
+        return self.ring
 
 
 class StepFn(nn.Module):

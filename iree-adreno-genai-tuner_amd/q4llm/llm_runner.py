@@ -55,8 +55,13 @@ def plan(n_prompt, max_new, chunk, buckets, max_ctx, use_max=False):
 
 @torch.no_grad()
 def run(model, prompt, max_new_tokens=32, chunk=128, buckets=(256, 512, 1024, 2048, 4096), schedule="bucketed",
-        stop_ids=(), warmup=1, caches=None, sync_timing=True):
-    """Generate with the llm_runner.c schedule; returns the runner's JSON report as a dict."""
+        stop_ids=(), warmup=1, caches=None, sync_timing=True, decode_steps=8):
+    """Generate with the llm_runner.c schedule; returns the runner's JSON report as a dict.
+
+    decode_steps > 1: while `decode_steps` more tokens fit in max_new_tokens and in the current bucket,
+    one graph replay runs that many decode steps (the model's multi-step entry point) and the host
+    reads their tokens back at once; tokens after a stop id are dropped (their steps only wrote cache
+    rows past the end of the sequence). The generated tokens are those of one step per replay."""
     buckets = sorted(buckets)
     use_max = schedule == "max"
     n_prompt = len(prompt)
@@ -70,6 +75,20 @@ def run(model, prompt, max_new_tokens=32, chunk=128, buckets=(256, 512, 1024, 20
             fns[(Cn, L)] = model.entry_point(Cn, L, caches)
         return fns[(Cn, L)]
 
+    def dec_fn(L, k):
+        if k == 1:
+            return fn(1, L)
+        if ("run", L, k) not in fns:
+            fns[("run", L, k)] = model.entry_point(1, L, caches, steps=k)
+        return fns[("run", L, k)]
+
+    def run_len(pos, n_have):
+        """decode steps of the next replay at position pos with n_have tokens generated"""
+        if decode_steps <= 1 or n_have + decode_steps > max_new_tokens:
+            return 1
+        L = pick_bucket(buckets, pos + 1, use_max)
+        return decode_steps if pick_bucket(buckets, pos + decode_steps, use_max) == L else 1
+
     # warm-up: every function the schedule uses; writes garbage KV at [0, C) that prefill overwrites
     t_warm = time.perf_counter()
     for _ in range(warmup):
@@ -77,6 +96,8 @@ def run(model, prompt, max_new_tokens=32, chunk=128, buckets=(256, 512, 1024, 20
             fn(chunk, L)([0] * chunk, 0, 0)
         for L in sorted(set(dec)):
             fn(1, L)([0], 0, 0)
+            if decode_steps > 1 and dec.count(L) >= decode_steps:
+                dec_fn(L, decode_steps)  # built (captured), not run
     torch.cuda.synchronize(dev)
     t_warm = time.perf_counter() - t_warm
 
@@ -100,17 +121,22 @@ def run(model, prompt, max_new_tokens=32, chunk=128, buckets=(256, 512, 1024, 20
         L = pick_bucket(buckets, pos + 1, use_max)
         if L < 0:
             break
+        k = run_len(pos, len(generated))
         ts = time.perf_counter()
-        g = fn(1, L)
+        g = dec_fn(L, k)
         if fed.get(id(g)) != (pos, generated[-1]):
-            g.start.fill_(pos)
-            g.tokens.fill_(generated[-1])
-        nxt = int(g.replay().item())
+            g.set_fed(pos, generated[-1])
+        out = g.replay()
+        toks = [int(out.item())] if k == 1 else out.tolist()
         if g.feeds_back:
-            fed[id(g)] = (pos + 1, nxt)
-        steps.append([L, (time.perf_counter() - ts) * 1e3])
-        generated.append(nxt)
-        pos += 1
+            fed[id(g)] = (pos + k, toks[-1])
+        ms = (time.perf_counter() - ts) * 1e3 / k
+        for t in toks:
+            steps.append([L, ms])
+            generated.append(t)
+            pos += 1
+            if t in stop_ids:
+                break
     decode_s = time.perf_counter() - t1
     n_steps = len(generated) - 1
     return {

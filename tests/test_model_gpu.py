@@ -92,6 +92,21 @@ def test_runner_ragged_prompt_and_stop_ids(dev):
     assert res2["tokens"] == want[: want.index(stop) + 1]
 
 
+def test_runner_multi_step_decode_matches_one_step(dev):
+    """Decode replays of 8 steps (one graph, one readback; single steps where a run would cross a
+    bucket or the end) give the oracle's tokens across bucket switches, as one-step replays do, and
+    their steps read the positions of the caches the one-step run writes."""
+    model, ref = build_pair(synth.TINY, 32, 128)
+    prompt = synth.prompt_ids(10, 1024, seed=8)
+    want = R.generate(ref, prompt, 60, 8, [16, 32, 64, 128])
+    c1, c8 = model.new_caches(), model.new_caches()
+    one = llm_runner.run(model, prompt, 60, 8, [16, 32, 64, 128], caches=c1, decode_steps=1)
+    run8 = llm_runner.run(model, prompt, 60, 8, [16, 32, 64, 128], caches=c8, decode_steps=8)
+    assert one["tokens"] == want and run8["tokens"] == want
+    for a, b in zip(c1, c8):  # rows 0 .. 68 written, the same values
+        assert torch.equal(a[:69], b[:69])
+
+
 def test_graph_replay_matches_eager_step(dev):
     """The captured entry point, replayed several times with eager work in between, equals step()."""
     model, _ = build_pair(synth.TINY, 32, 128)
