@@ -269,7 +269,6 @@ __global__ __launch_bounds__(256) void attn_combine8_kernel(const float* __restr
                                                           int S, const int32_t* __restrict__ start_p,
                                                           uint16_t* __restrict__ xh, uint16_t* __restrict__ xl) {
   constexpr int kB = 8, D8 = HD / 8;
-  typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;

@@ -22,7 +22,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32
 // The whole vector is bit-cast: bit-casting single elements of the loaded vector compiled to four
 // copies of element 0 with this compiler.
 __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const f32x4 f = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   return make_float4(f.x, f.y, f.z, f.w);

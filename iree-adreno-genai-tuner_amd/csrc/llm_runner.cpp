@@ -4,6 +4,7 @@
 //   llm-runner --weights=model.q4w --prompt=ids.txt [--max_new_tokens=32] [--chunk=128]
 //              [--buckets=256,512,1024,2048,4096] [--schedule=bucketed|max] [--n_layers=N]
 //              [--n_kv_heads=N] [--head_dim=N] [--max_ctx=N] [--stop_ids=a,b] [--warmup=1] [--plan]
+//              [--decode_steps=8]
 //
 // Kept from llm_runner.c (same flag names and meaning, same schedule, same JSON keys):
 //   * prefill in chunks of --chunk tokens, the last chunk zero-padded, last = n - 1 of the chunk;
@@ -20,6 +21,10 @@
 // (q4llm/packed.py) copied once to HBM, and each entry point prefill_c{C}_l{L} / decode_l{L} is one
 // q4llm_step captured into a HIP graph on first use and replayed; per call the host copies the
 // token ids, start and last into pinned buffers, launches the graph and reads back 4 bytes.
+// --decode_steps=K (default 8; 1 = one step per launch): while K more tokens fit in --max_new_tokens
+// and in the current bucket, one graph of K self-feeding decode steps runs per launch and the host
+// reads the K tokens back at once; tokens after a stop id are dropped (their steps only wrote cache
+// rows past the end of the sequence), so the output is that of one step per launch.
 // --plan prints the schedule (the buckets of every prefill chunk and decode step) and exits
 // without touching the GPU.
 #include <hip/hip_runtime.h>
@@ -43,6 +48,7 @@ namespace {
 struct Flags {
   std::string weights, prompt, buckets = "256,512,1024,2048,4096", schedule = "bucketed", stop_ids;
   int max_new_tokens = 32, chunk = 128, n_layers = -1, n_kv_heads = -1, head_dim = -1, max_ctx = -1, warmup = 1;
+  int decode_steps = 8;
   bool plan = false;
 };
 
@@ -124,11 +130,13 @@ Flags parse_flags(int argc, char** argv) {
     else if (key == "head_dim") num(&f.head_dim);
     else if (key == "max_ctx") num(&f.max_ctx);
     else if (key == "warmup") num(&f.warmup);
+    else if (key == "decode_steps") num(&f.decode_steps);
     else if (key == "plan") f.plan = val.empty() || val == "1" || val == "true";
     else die("unknown flag --%s", key.c_str());
   }
   if (f.schedule != "bucketed" && f.schedule != "max") die("--schedule must be bucketed or max, not %s", f.schedule.c_str());
   if (f.chunk <= 0) die("--chunk must be positive");
+  if (f.decode_steps <= 0) die("--decode_steps must be positive");
   return f;
 }
 
@@ -270,6 +278,20 @@ struct EntryPoint {
   int32_t fed_start = 0, fed_token = 0;
 };
 
+// K decode steps in one graph: step i reads the token in ring slot i - 1 (step 0: the last slot,
+// the previous launch's last token) and writes its next token into slot i; every step is
+// q4llm_step_feed, so a launch ends with start advanced by K and the inputs set for the next one.
+struct DecodeRun {
+  int L = 0, K = 0;
+  int32_t* io = nullptr;  // device [K + 2]: ring[K], start, last
+  int32_t *ring = nullptr, *start = nullptr, *last = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipGraphExec_t exec = nullptr;
+  bool fed = false;
+  int32_t fed_start = 0, fed_token = 0;
+};
+
 struct Runner {
   q4llm_model model{};
   std::vector<q4llm_layer> layers;
@@ -278,6 +300,7 @@ struct Runner {
   int32_t* host = nullptr;  // pinned: [0, C) tokens, then start, last, next
   int host_cap = 0;
   std::map<std::pair<int, int>, EntryPoint> eps;
+  std::map<std::pair<int, int>, DecodeRun> runs;
 
   // decode entry points (feed) advance their own start in the step's last kernel
   void raw_step(EntryPoint& e, bool feed = false) {
@@ -321,6 +344,62 @@ struct Runner {
     HIP_OK(hipGraphInstantiate(&e.exec, g, nullptr, nullptr, 0));
     HIP_OK(hipGraphDestroy(g));
     return eps.emplace(key, e).first->second;
+  }
+
+  DecodeRun& run_entry(int L, int K) {
+    auto key = std::make_pair(L, K);
+    auto it = runs.find(key);
+    if (it != runs.end()) return it->second;
+    DecodeRun d;
+    d.L = L;
+    d.K = K;
+    HIP_OK(hipMalloc(&d.io, sizeof(int32_t) * (K + 2)));
+    HIP_OK(hipMemset(d.io, 0, sizeof(int32_t) * (K + 2)));
+    d.ring = d.io;
+    d.start = d.io + K;
+    d.last = d.start + 1;
+    Q4_OK_OR_DIE(q4llm_step_workspace_bytes(&model, 1, L, &d.ws_bytes));
+    HIP_OK(hipMalloc(&d.ws, d.ws_bytes));
+    HIP_OK(hipMemset(d.ws, 0, d.ws_bytes));
+    // set-up launch outside capture at position max_ctx (no cache row written), as in entry()
+    const int32_t setup_pos = model.max_ctx;
+    HIP_OK(hipMemcpy(d.start, &setup_pos, sizeof(int32_t), hipMemcpyHostToDevice));
+    Q4_OK_OR_DIE(q4llm_step(&model, d.ring + K - 1, 1, d.start, d.last, caches.data(), L, d.ring, nullptr, d.ws,
+                            d.ws_bytes, stream));
+    HIP_OK(hipStreamSynchronize(stream));
+    HIP_OK(hipMemset(d.io, 0, sizeof(int32_t) * (K + 2)));
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < K; ++i)
+      Q4_OK_OR_DIE(q4llm_step_feed(&model, d.ring + (i + K - 1) % K, 1, d.start, d.last, caches.data(), L,
+                                   d.ring + i, nullptr, d.ws, d.ws_bytes, stream));
+    HIP_OK(hipStreamEndCapture(stream, &g));
+    HIP_OK(hipGraphInstantiate(&d.exec, g, nullptr, nullptr, 0));
+    HIP_OK(hipGraphDestroy(g));
+    return runs.emplace(key, d).first->second;
+  }
+
+  // K decode steps from position start after token `token`: the K next tokens into out[0, K).
+  void call_run(int L, int K, int32_t token, int start, int32_t* out) {
+    DecodeRun& d = run_entry(L, K);
+    if (K + 2 > host_cap) {
+      if (host) HIP_OK(hipHostFree(host));
+      host_cap = K + 2;
+      HIP_OK(hipHostMalloc(reinterpret_cast<void**>(&host), sizeof(int32_t) * host_cap, hipHostMallocDefault));
+    }
+    if (!(d.fed && d.fed_start == start && d.fed_token == token)) {
+      host[0] = token;  // -> ring[K - 1]
+      host[1] = start;
+      host[2] = 0;  // last
+      HIP_OK(hipMemcpyAsync(d.ring + K - 1, host, sizeof(int32_t) * 3, hipMemcpyHostToDevice, stream));
+    }
+    HIP_OK(hipGraphLaunch(d.exec, stream));
+    HIP_OK(hipMemcpyAsync(host, d.ring, sizeof(int32_t) * K, hipMemcpyDeviceToHost, stream));
+    HIP_OK(hipStreamSynchronize(stream));
+    for (int i = 0; i < K; ++i) out[i] = host[i];
+    d.fed = true;
+    d.fed_start = start + K;
+    d.fed_token = out[K - 1];
   }
 
   // One call of the entry point: token ids, start and last in, the greedy next token out.
@@ -490,6 +569,9 @@ int main(int argc, char** argv) {
           r.call(1, L, zeros.data(), 1, 0, 0);
           break;
         }
+      // the K-step graph of a bucket that holds K decode steps: built (captured), not run
+      if (f.decode_steps > 1 && std::count(used_dec.begin(), used_dec.end(), L) >= f.decode_steps)
+        r.run_entry(L, f.decode_steps);
     }
   }
   const double warm_ms = now_ms() - tw;
@@ -517,12 +599,30 @@ int main(int argc, char** argv) {
     if (stop) break;
     const int L = pick_bucket(buckets, pos + 1, use_max);
     if (L < 0) break;
+    const int K = f.decode_steps;
+    const bool run = K > 1 && static_cast<int>(generated.size()) + K <= f.max_new_tokens &&
+                     pick_bucket(buckets, pos + K, use_max) == L;
     const double ts = now_ms();
     const int32_t tok = next;
-    next = r.call(1, L, &tok, 1, pos, 0);
-    steps.emplace_back(L, now_ms() - ts);
-    generated.push_back(next);
-    ++pos;
+    if (!run) {
+      next = r.call(1, L, &tok, 1, pos, 0);
+      steps.emplace_back(L, now_ms() - ts);
+      generated.push_back(next);
+      ++pos;
+      continue;
+    }
+    std::vector<int32_t> outs(K);
+    r.call_run(L, K, tok, pos, outs.data());
+    const double per = (now_ms() - ts) / K;
+    for (int i = 0; i < K; ++i) {
+      next = outs[i];
+      steps.emplace_back(L, per);
+      generated.push_back(next);
+      ++pos;
+      bool hit = false;
+      for (int s : stops) hit = hit || next == s;
+      if (hit) break;
+    }
   }
   const double decode_ms = now_ms() - t1;
   const int n_steps = static_cast<int>(generated.size()) - 1;
@@ -543,6 +643,11 @@ int main(int argc, char** argv) {
   std::fflush(stdout);
 
   for (auto& kv : r.eps) {
+    HIP_OK(hipGraphExecDestroy(kv.second.exec));
+    HIP_OK(hipFree(kv.second.ws));
+    HIP_OK(hipFree(kv.second.io));
+  }
+  for (auto& kv : r.runs) {
     HIP_OK(hipGraphExecDestroy(kv.second.exec));
     HIP_OK(hipFree(kv.second.ws));
     HIP_OK(hipFree(kv.second.io));

@@ -91,6 +91,24 @@ def test_native_runner_no_warmup_keeps_live_kv(packed_file, tmp_path):
     assert res["tokens"] == py["tokens"]
 
 
+def test_native_runner_multi_step_decode(packed_file, tmp_path):
+    """--decode_steps: launches of 8 (or 5) self-feeding decode steps, single steps next to the bucket
+    switches and the end, give the one-step runner's tokens; a stop id inside a launch ends the
+    output at that token."""
+    p, model = packed_file
+    prompt = synth.prompt_ids(10, 1024, seed=8)
+    flags = ("--max_new_tokens=60", "--chunk=8", "--buckets=16,32,64,128")
+    one = run_native(p, prompt, tmp_path, *flags, "--decode_steps=1")
+    py = llm_runner.run(model, prompt, 60, 8, [16, 32, 64, 128], decode_steps=1)
+    assert one["tokens"] == py["tokens"]
+    for k in (8, 5):
+        assert run_native(p, prompt, tmp_path, *flags, f"--decode_steps={k}")["tokens"] == one["tokens"], k
+    stop = one["tokens"][30]
+    first = one["tokens"].index(stop)
+    got = run_native(p, prompt, tmp_path, *flags, "--decode_steps=8", f"--stop_ids={stop}")
+    assert got["tokens"] == one["tokens"][: first + 1]
+
+
 def test_context_sweep_records(packed_file, tmp_path):
     """q4llm.sweep (scripts/llm/bench.py:69-107 contract): one record per (kind, ctx, schedule) with
     the runner's keys plus kind/ctx/tag, and the summary table over them."""
