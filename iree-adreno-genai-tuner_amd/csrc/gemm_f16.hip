@@ -446,6 +446,8 @@ constexpr TileCfg kTiles[] = {
     {64, 96, 2, 3, 4, 64, true},    // 3: 6 waves of 32x32, 4 stages (81 KB), pipelined: M = 256, N = 5120 on 216 CUs
     {128, 64, 2, 2, 4, 64},         // 4: 4 waves of 64x32, 4 stages (96 KB)
     {64, 64, 2, 2, 4, 64},          // 5: 4 waves of 32x32, 4 stages (64 KB)
+    {128, 160, 2, 5, 4, 64, true},  // 6: 10 waves of 64x32, 4 stages (145 KB), pipelined: M = 1024, N = 5120
+                                    //    in exactly 256 tiles
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -462,17 +464,21 @@ constexpr size_t gemm_lds() {
   constexpr TileCfg t = kTiles[I];
   return GemmCfg<t.bm, t.bn, t.wgm, t.wgn, t.nst, t.bk>::kLds;
 }
-constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(), gemm_fn<4>(), gemm_fn<5>()};
-constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(), gemm_lds<4>(),
-                               gemm_lds<5>()};
+constexpr GemmFn kGemmFns[] = {gemm_fn<0>(), gemm_fn<1>(), gemm_fn<2>(), gemm_fn<3>(),
+                               gemm_fn<4>(), gemm_fn<5>(), gemm_fn<6>()};
+constexpr size_t kGemmLds[] = {gemm_lds<0>(), gemm_lds<1>(), gemm_lds<2>(), gemm_lds<3>(),
+                               gemm_lds<4>(), gemm_lds<5>(), gemm_lds<6>()};
 static_assert(sizeof(kGemmFns) / sizeof(kGemmFns[0]) == kNumTiles, "one kernel per tile entry");
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Fixed rule, from sweeps of every entry (and K splits of 1-8) over the config-3 shapes on one
 // MI355X (graph replays, weights rotated past the MALL):
-//   * M >= 512: 256x256 when that alone fills the 256 CUs (4096^3: 1.05 PFLOP/s), else 128x128 with
-//     two workgroups per CU (2048x3072x8192: 117 us); K splits only lost here;
+//   * M >= 512: 256x256 when that alone fills the 256 CUs (4096^3: 1.05 PFLOP/s); else the pipelined
+//     128x160 entry when its tiles make one round of 240-256 workgroups (1024x5120x3072: 256 tiles,
+//     46.0 -> 41.7 us against 128x128); else 128x128 with two workgroups per CU (2048x3072x8192:
+//     117 us; 128x160 there gives 320 tiles, 179 us, and 128x192 256 tiles, 129 us); K splits only
+//     lost here;
 //   * M < 512 with a workspace (gemm_f16_nt_ws): the pipelined 128x128 entry with K split so the
 //     tiles times the split come closest to 256 workgroups (256x5120x3072: 80 tiles x 3, 23.1 us;
 //     256x3072x8192: 48 x 5, 29 us; 256x16384x3072: 256 x 1, 40 us);
@@ -491,7 +497,7 @@ int choose_tile(int64_t M, int64_t N, bool split_ok) {
     if (i >= 0 && i < kNumTiles) return i;
   }
   auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
-  if (M >= 512) return tiles(0) >= 256 ? 0 : 1;
+  if (M >= 512) return tiles(0) >= 256 ? 0 : (tiles(6) >= 240 && tiles(6) <= 256 ? 6 : 1);
   if (split_ok && N % 4 == 0) return 2;
   if (tiles(2) >= 160) return 2;
   // 64x96 when it covers the CUs in one round (256x5120x3072: 160 workgroups of 128x64 -> 216 of 64x96,
