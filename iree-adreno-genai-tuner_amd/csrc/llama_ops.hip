@@ -277,15 +277,32 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
 }
 
 // The same into the fp16 (hi, lo) planes of the down projection: one thread per 8-element chunk
-// (inter % 8 == 0), two 16-byte loads of gate and of up, one 16-byte store per plane.
+// (inter % 8 == 0), two 16-byte loads of gate and of up, one 16-byte store per plane. With n_split > 0
+// each of the four 16-byte values is the sum of the n_split partials part[s] ([M, 2 inter] each) in
+// ascending order (sum_partials4, as linear_reduce_kernel adds them), and gu is not read.
 __global__ __launch_bounds__(256) void silu_mul_planes_kernel(const float* __restrict__ gu, uint16_t* __restrict__ xh,
-                                                              uint16_t* __restrict__ xl, int64_t M, int64_t inter) {
+                                                              uint16_t* __restrict__ xl, int64_t M, int64_t inter,
+                                                              const float* __restrict__ part, int n_split) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // chunk of the [M, inter] result
   if (c >= M * inter / 8) return;
   const int64_t m = (8 * c) / inter, i = (8 * c) % inter;
-  const float4* gp = reinterpret_cast<const float4*>(gu + m * 2 * inter + i);
-  const float4* up = reinterpret_cast<const float4*>(gu + m * 2 * inter + inter + i);
-  const float4 g0 = gp[0], g1 = gp[1], u0 = up[0], u1 = up[1];
+  const int64_t g_off = m * 2 * inter + i, u_off = g_off + inter;
+  float4 g0, g1, u0, u1;
+  if (n_split > 0) {
+    const int64_t stride = M * 2 * inter / 4;  // one partial, in float4
+    const float4* p4 = reinterpret_cast<const float4*>(part);
+    g0 = sum_partials4(p4 + g_off / 4, stride, n_split);
+    g1 = sum_partials4(p4 + g_off / 4 + 1, stride, n_split);
+    u0 = sum_partials4(p4 + u_off / 4, stride, n_split);
+    u1 = sum_partials4(p4 + u_off / 4 + 1, stride, n_split);
+  } else {
+    const float4* gp = reinterpret_cast<const float4*>(gu + g_off);
+    const float4* up = reinterpret_cast<const float4*>(gu + u_off);
+    g0 = gp[0];
+    g1 = gp[1];
+    u0 = up[0];
+    u1 = up[1];
+  }
   const float e8[8] = {silu_mul1(g0.x, u0.x), silu_mul1(g0.y, u0.y), silu_mul1(g0.z, u0.z), silu_mul1(g0.w, u0.w),
                        silu_mul1(g1.x, u1.x), silu_mul1(g1.y, u1.y), silu_mul1(g1.z, u1.z), silu_mul1(g1.w, u1.w)};
   store_x_planes8(xh, xl, c, e8);
@@ -463,12 +480,14 @@ int rope_kv_partials(float* qkv, const float* part, int n_split, const float* co
   return launch_status();
 }
 
-int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st) {
-  if (!gu || !xh || !xl) return Q4_ERR_NULL;
-  if (M <= 0 || inter <= 0 || inter % 8) return Q4_ERR_SHAPE;
-  if (!aligned(gu, 16) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
+int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st,
+                    const float* part, int n_split) {
+  if (n_split > 0 ? !part : !gu) return Q4_ERR_NULL;
+  if (!xh || !xl) return Q4_ERR_NULL;
+  if (M <= 0 || inter <= 0 || inter % 8 || n_split < 0) return Q4_ERR_SHAPE;
+  if ((n_split > 0 ? !aligned(part, 16) : !aligned(gu, 16)) || !aligned(xh, 16) || !aligned(xl, 16)) return Q4_ERR_ALIGN;
   hipLaunchKernelGGL(silu_mul_planes_kernel, dim3(static_cast<unsigned>((M * inter / 8 + 255) / 256)), dim3(256), 0,
-                     st, gu, xh, xl, M, inter);
+                     st, gu, xh, xl, M, inter, part, n_split);
   return launch_status();
 }
 

@@ -94,8 +94,11 @@ bool rope_kv_takes_partials(const float* qkv, const float* cos_t, const float* s
                             const uint16_t* vc, int hd);
 int rope_kv_partials(float* qkv, const float* part, int n_split, const float* cos_t, const float* sin_t, uint16_t* kc,
                      uint16_t* vc, int C, int n_q, int n_kv, int hd, int max_ctx, const int32_t* start, hipStream_t st);
-// silu_mul_f32, written as planes.
-int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st);
+// silu_mul_f32, written as planes. With n_split > 0 gu is not read: gate and up are the sums of the
+// n_split K-split partials `part` ([M, 2 inter] fp32 each) of the gate/up projection, added in the
+// order of linear_reduce_kernel.
+int silu_mul_planes(const float* gu, uint16_t* xh, uint16_t* xl, int64_t M, int64_t inter, hipStream_t st,
+                    const float* part = nullptr, int n_split = 0);
 // attn_bucket for C > 1, its output written as planes.
 int attn_bucket_planes(const float* q, int q_row_stride, const uint16_t* k_cache, const uint16_t* v_cache,
                        uint16_t* xh, uint16_t* xl, int C, int n_q, int n_kv, int hd, int L, const int32_t* start,

@@ -359,7 +359,8 @@ __device__ __forceinline__ float silu_mul_exact(float g, float u) {
 // and head size it was packed with). Columns are virtual rows: a 64-k stage of 32 of them is half of
 // each 64-byte row of two 16-row tiles (16 cache lines per 1 KB load instead of 32 in the reference
 // layout), a group's scales of a tile are 32 contiguous bytes, and the epilogue writes each virtual
-// column to its weight row (SwiGLU: gate and up of a pair sit 8 columns apart, exchanged by DPP).
+// column to its weight row (EPI 1 on the SwiGLU pairing: gate and up of a pair sit 8 columns apart,
+// exchanged by DPP).
 template <int BM, int BN, int WM, int WN, int NST, int KS, int EPI = 0, bool PIPE = false, bool T16 = false>
 __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
     const uint16_t* __restrict__ XH, const uint16_t* __restrict__ XL, const int32_t* __restrict__ QW,
@@ -844,6 +845,10 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void q4_linear_ws_kernel(
             const int pr = 8 * (col >> 4) + (col & 7), hh = t16_hd >> 1, sh = __builtin_ctz(hh);
             const int head = pr >> sh;
             col = pr < (N >> 1) ? head * t16_hd + (pr - (head << sh)) + ((col & 8) ? hh : 0) : N;
+          } else if (t16_pair == Q4_PAIR_SWIGLU) {
+            // virtual column -> pair p = 8 (c / 16) + c % 8: gate row p, or up row N / 2 + p
+            const int pr = 8 * (col >> 4) + (col & 7);
+            col = pr < (N >> 1) ? pr + ((col & 8) ? (N >> 1) : 0) : N;
           }
         }
         if (row < M && col < N) {
@@ -912,7 +917,7 @@ bool t16_usable(const T16Src* t, int64_t N, int group, int pairing_needed) {
   if (!t || !t->tiles || !t->scales || getenv("Q4_PREFILL_REF_LAYOUT")) return false;
   if ((group != 32 && group != 128) || !aligned(t->tiles, 16) || !aligned(t->scales, 4)) return false;
   if (pairing_needed >= 0 && t->pairing != pairing_needed) return false;
-  if (t->pairing == Q4_PAIR_SWIGLU) return pairing_needed == Q4_PAIR_SWIGLU && N % 16 == 0;
+  if (t->pairing == Q4_PAIR_SWIGLU) return N % 16 == 0;
   if (t->pairing == Q4_PAIR_ROPE) {
     const int hh = t->head_dim / 2;
     return N % 16 == 0 && t->head_dim > 0 && hh % 8 == 0 && (hh & (hh - 1)) == 0 && N % t->head_dim == 0;

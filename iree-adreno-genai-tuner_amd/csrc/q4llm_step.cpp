@@ -277,9 +277,12 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
                                     lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));
       } else {
         if (fused != Q4_ERR_UNSUPPORTED) return fused;
+        // a K split of gate/up is added by the silu_mul kernel (Q4_SWIGLU_UNFUSED set: by its own
+        // reduce kernel first); same sums, same order
+        int gu_split = 0;
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st, part,
-                                    lo.part_bytes));
-        Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st));
+                                    lo.part_bytes, getenv("Q4_SWIGLU_UNFUSED") ? nullptr : &gu_split, &wgu_t));
+        Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st, part, gu_split));
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
                                     lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));
       }

@@ -161,19 +161,26 @@ def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch
     assert (l_f.cpu() - r_l).abs().max().item() <= tol(r_l)
 
 
-def test_prefill_chunk128_k_split_paths_vs_oracle(dev):
+def test_prefill_chunk128_k_split_paths_vs_oracle(dev, monkeypatch):
     """A 128-row chunk takes every K-split path of the prefill step: qkv, o and down split and completed
     by the RoPE / rms_norm kernels after them, and gate/up (too few 64x256 tiles at 128 rows for its
-    SwiGLU epilogue) split and reduced by its own kernel before silu_mul. Two chunks (the second reading
-    the first's caches), next token and logits against the oracle."""
+    SwiGLU epilogue) split 2 ways, its partials added by the silu_mul kernel: bit-identical to adding
+    them with the reduce kernel first (Q4_SWIGLU_UNFUSED). Two chunks (the second reading the first's
+    caches), next token and logits against the oracle."""
     cfg = dict(synth.TINY, intermediate_size=8192, num_hidden_layers=2)
     ours, ref = build_pair(cfg, 32, 256)
     prompt = synth.prompt_ids(256, cfg["vocab_size"], seed=5)
-    c_ours, c_ref = ours.new_caches(), ref.new_caches()
+    c_ours, c_two, c_ref = ours.new_caches(), ours.new_caches(), ref.new_caches()
     for s0 in (0, 128):
         toks = torch.tensor([prompt[s0:s0 + 128]], dtype=torch.int32)
         start, last = torch.tensor([s0], dtype=torch.int32), torch.tensor([127], dtype=torch.int32)
         n_o, l_o = ours.step(toks, start, last, c_ours, 256)
+        monkeypatch.setenv("Q4_SWIGLU_UNFUSED", "1")
+        n_t, l_t = ours.step(toks, start, last, c_two, 256)
+        monkeypatch.delenv("Q4_SWIGLU_UNFUSED")
+        assert torch.equal(l_o, l_t) and int(n_o.item()) == int(n_t.item()), s0
+        for a, b in zip(c_ours, c_two):
+            assert torch.equal(a, b), s0
         r_n, r_l = ref.step(toks, start, last, c_ref, 256)
         assert int(n_o.item()) == int(r_n.item()), s0
         assert (l_o.cpu() - r_l).abs().max().item() <= tol(r_l), s0

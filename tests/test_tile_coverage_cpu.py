@@ -527,8 +527,9 @@ def t16_pack(qbytes, sc, N, K, group, pairing, hd):
 def test_linear_ws_t16_loads_and_outputs(pairing, N, K, group):
     """Every 1 KB weight load of a 64-k stage of 32 virtual columns brings, for LDS row r (lane / 2), the
     64 nibbles of weight row t16_row(column) at that stage; every scale slot holds the fp16 scale of that
-    row and the stage's group; and the epilogue writes each virtual column to t16_row (RoPE, none) or,
-    for SwiGLU, each pair once from the lane holding gate with up 8 columns away."""
+    row and the stage's group; and the epilogue writes each virtual column to t16_row (EPI 0, every
+    pairing) and, for the SwiGLU epilogue, each pair once from the lane holding gate with up 8 columns
+    away."""
     hd = 64
     cfg = config_table("linear_ws")[-1]
     bm, bn, wm, wn, nst, ks_n, pipe = cfg
@@ -584,6 +585,15 @@ def test_linear_ws_t16_loads_and_outputs(pairing, N, K, group):
                 if vc < 16 * n_t16 and pr < N // 2:
                     assert t16_row(gate_c, N, 1, hd) == pr and t16_row(up_c, N, 1, hd) == pr + N // 2
                     seen[pr] += 1
+        assert (seen == 1).all()
+        # EPI 0 (K-split partials, or gate/up before a separate SwiGLU): each virtual column to its row
+        seen = np.zeros(N, np.int32)
+        for vc in cols:
+            pr = 8 * (vc >> 4) + (vc & 7)
+            col = pr + (N // 2 if vc & 8 else 0) if pr < N // 2 else N
+            if col < N:
+                assert col == t16_row(vc, N, 1, hd)
+                seen[col] += 1
         assert (seen == 1).all()
     else:
         seen = np.zeros(N, np.int32)
