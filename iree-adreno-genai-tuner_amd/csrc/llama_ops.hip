@@ -58,9 +58,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
 #pragma unroll
     for (int i = 0; i < kV; ++i) wv[i] = load_f4(wres, (threadIdx.x + i * 256) * 16u);
     if (n_split > 0) {
-      // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row, the sums run
+      // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row (a K split
+      // of the 3B prefill's o and down projections has 5 at 256 rows, 8 and 10 at 128), the sums run
       // in ascending split order, as in linear_reduce_kernel
-      constexpr int kPb = 6;
+      constexpr int kPb = 12;
       const uint32_t row_bytes = static_cast<uint32_t>(D) * 4u;
       const uint32_t plane_bytes = static_cast<uint32_t>(M * D) * 4u;
       const __amdgpu_buffer_rsrc_t pres = row_rsrc(psum, plane_bytes * static_cast<uint32_t>(n_split));
