@@ -34,7 +34,10 @@ __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off
 // With xh != nullptr the row goes to the fp16 (hi, lo) planes of a prefill projection instead of out.
 // With n_split > 0 (rows held in registers only) x is first completed with the K-split partials of the
 // projection that produced it, x += psum[0] + ... + psum[n_split - 1] (each [M, D]; the order of
-// linear_reduce_kernel, so the same bits), and the completed row is written back to x.
+// linear_reduce_kernel, so the same bits), and the completed row is written back to x. The first PB
+// partials load with the row, the rest one round trip each (PB 12 for more than 6 partials: the 128-row
+// prefill chunks have 8 and 10; 6 otherwise, where the 12-wide form measured 1.3% slower prefill).
+template <int PB = 6>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
                                                       const int32_t* __restrict__ row_sel,
@@ -58,10 +61,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
 #pragma unroll
     for (int i = 0; i < kV; ++i) wv[i] = load_f4(wres, (threadIdx.x + i * 256) * 16u);
     if (n_split > 0) {
-      // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row (a K split
-      // of the 3B prefill's o and down projections has 5 at 256 rows, 8 and 10 at 128), the sums run
+      // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row, the sums run
       // in ascending split order, as in linear_reduce_kernel
-      constexpr int kPb = 12;
+      constexpr int kPb = PB;
       const uint32_t row_bytes = static_cast<uint32_t>(D) * 4u;
       const uint32_t plane_bytes = static_cast<uint32_t>(M * D) * 4u;
       const __amdgpu_buffer_rsrc_t pres = row_rsrc(psum, plane_bytes * static_cast<uint32_t>(n_split));
@@ -406,7 +408,7 @@ extern "C" int rmsnorm_f32(const float* x, const float* w, float* out, int64_t M
   if (M <= 0 || D <= 0) return Q4_ERR_SHAPE;
   if (D % 4 == 0 && (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16))) return Q4_ERR_ALIGN;
   const unsigned grid = row ? 1u : static_cast<unsigned>(M);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row,
+  hipLaunchKernelGGL(rmsnorm_kernel<>, dim3(grid), dim3(256), 0, as_stream(stream), x, w, out, M, D, eps, row,
                      nullptr, nullptr);
   return launch_status();
 }
@@ -448,8 +450,12 @@ int rmsnorm_planes(float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t
   if (n_split > 0 && (!part || !aligned(part, 16) || !rmsnorm_takes_partials(D) ||
                       static_cast<int64_t>(n_split) * M * D * 4 >= (int64_t{1} << 31)))
     return Q4_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
-                     nullptr, xh, xl, part, n_split);
+  if (n_split > 6)
+    hipLaunchKernelGGL(rmsnorm_kernel<12>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
+                       nullptr, xh, xl, part, n_split);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<6>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
+                       nullptr, xh, xl, part, n_split);
   return launch_status();
 }
 
@@ -459,8 +465,12 @@ int rmsnorm_row_partials(float* x, const float* w, float* out, int64_t M, int64_
   if (M <= 0 || D <= 0 || n_split <= 0 || !rmsnorm_takes_partials(D)) return Q4_ERR_SHAPE;
   if (static_cast<int64_t>(n_split) * M * D * 4 >= (int64_t{1} << 31)) return Q4_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || !aligned(part, 16)) return Q4_ERR_ALIGN;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, st, x, w, out, M, D, eps, row, nullptr, nullptr, part,
-                     n_split);
+  if (n_split > 6)
+    hipLaunchKernelGGL(rmsnorm_kernel<12>, dim3(1), dim3(256), 0, st, x, w, out, M, D, eps, row, nullptr, nullptr, part,
+                       n_split);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<6>, dim3(1), dim3(256), 0, st, x, w, out, M, D, eps, row, nullptr, nullptr, part,
+                       n_split);
   return launch_status();
 }
 
