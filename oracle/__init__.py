@@ -11,12 +11,19 @@ How each part is pinned (checks live in tests/test_oracle.py):
                                            rounding, bit 31, all 16 nibble values), invariants.
   gemv_fused / QLinearRef                  fp64 textbook matvec on the dequantized weight; the
                                            fused and eager forms agree (qgemv_test.py:13-19).
-  attention inside step                    fp64 brute-force softmax; single-key and equal-key
-                                           closed forms.
+  attention                                closed forms (one valid key returns that V row bit for
+                                           bit per GQA group; equal keys give the mean of V; two
+                                           keys give sigmoid weights, which pins the scale); rows
+                                           past pos changed to large values leave the output
+                                           identical; fp64 brute force on a causal prefill chunk.
   rope_tables                              transformers' LlamaRotaryEmbedding (the reference's own
                                            source of the tables, llama_q4.py:184-192).
   LlamaQ4Ref.step (whole model)            transformers' LlamaForCausalLM on the same dequantized
                                            weights, the scripts/llm/test_tiny.py protocol: equal
                                            greedy tokens and |dlogit| < 1e-3.
   pick_bucket / schedule                   closed-form bucket sequences (llm_runner.c:143-245).
+  generate                                 its recorded (phase, start, L) calls, padding, `last`
+                                           and fed-back tokens equal schedule_calls on ragged
+                                           prompts, bucket switches, 'max', running out of
+                                           buckets and stop ids.
 """

@@ -166,6 +166,147 @@ def test_schedule_tiny_and_ragged_prompt():
     assert dec[0] == ("decode", 21, 32) and len(dec) == 9
 
 
+class _RecordingModel:
+    """Stands in for LlamaQ4Ref inside R.generate: records every step's (phase, start, L, C, last)
+    and answers with a scripted token per call, so the call sequence can be checked against the
+    closed-form schedule (llm_runner.c:210-245) without any arithmetic."""
+
+    def __init__(self, n_prompt, answers):
+        self.n_prompt, self.answers, self.calls = n_prompt, list(answers), []
+
+    def new_caches(self):
+        return []
+
+    def step(self, tokens, start, last, caches, L):
+        s = int(start[0])
+        self.calls.append(("prefill" if s < self.n_prompt else "decode", s, L, tokens.shape[1], int(last[0]),
+                           tokens[0].tolist()))
+        return torch.tensor([self.answers[len(self.calls) - 1]], dtype=torch.int32), None
+
+
+@pytest.mark.parametrize("n_prompt,max_new,chunk,buckets,use_max", [
+    (21, 10, 8, [16, 32, 64], False),        # ragged last chunk, bucket switch 16 -> 32 inside prefill
+    (16, 40, 16, [32, 64], False),           # decode crosses the 32 -> 64 bucket switch
+    (512, 256, 256, [256, 512, 1024, 2048, 4096], False),
+    (30, 12, 8, [16, 32, 64], True),         # 'max' schedule
+    (5, 70, 4, [16, 32, 64], False),         # runs out of buckets before max_new
+])
+def test_generate_calls_equal_closed_form_schedule(n_prompt, max_new, chunk, buckets, use_max):
+    """R.generate's (phase, start, L) sequence equals R.schedule_calls; prefill chunks are zero-padded
+    with last = (real rows - 1); each decode step feeds back the previous answer (llm_runner.c:210-245)."""
+    prompt = [(7 * i + 3) % 97 + 1 for i in range(n_prompt)]
+    answers = [1000 + i for i in range(400)]
+    m = _RecordingModel(n_prompt, answers)
+    out = R.generate(m, prompt, max_new, chunk, buckets, use_max=use_max)
+    want = R.schedule_calls(n_prompt, max_new, chunk, buckets, use_max)
+    assert [(p, s, L) for p, s, L, *_ in m.calls] == want
+    n_pre = len([c for c in want if c[0] == "prefill"])
+    for i, (_, s, _, C, last, toks) in enumerate(m.calls[:n_pre]):
+        real = min(chunk, n_prompt - s)
+        assert C == chunk and last == real - 1
+        assert toks == prompt[s:s + real] + [0] * (chunk - real)
+    for j, (_, s, _, C, last, toks) in enumerate(m.calls[n_pre:]):
+        assert C == 1 and last == 0 and s == n_prompt + j
+        assert toks == [answers[n_pre - 1 + j]]
+    assert out == answers[n_pre - 1:len(m.calls)]
+    assert len(out) == min(max_new, 1 + len(want) - n_pre)
+
+
+def test_generate_stops_after_stop_id_across_bucket_switch():
+    """A stop id produced at decode step j ends generation after that token: the call sequence is the
+    closed-form schedule cut right after the call that produced it (llm_runner.c:239-241)."""
+    n_prompt, chunk, buckets = 21, 8, [16, 32, 64]
+    want = R.schedule_calls(n_prompt, 30, chunk, buckets)
+    n_pre = 3
+    assert [L for _, _, L in want[n_pre:]].index(64) == 11     # decode step 11 is the first at L = 64
+    for stop_call in (n_pre - 1, n_pre + 10, n_pre + 11, n_pre + 12):
+        answers = [500 + i for i in range(64)]
+        answers[stop_call] = 2
+        m = _RecordingModel(n_prompt, answers)
+        out = R.generate(m, list(range(1, n_prompt + 1)), 30, chunk, buckets, stop_ids=(2, 9))
+        assert [(p, s, L) for p, s, L, *_ in m.calls] == want[:stop_call + 1]
+        assert out[-1] == 2 and out == answers[n_pre - 1:stop_call + 1]
+
+
+# ------------------------------------------------------------------------------------------------
+# a7: attention closed forms (llama_q4.py:204-232)
+# ------------------------------------------------------------------------------------------------
+
+
+def _attn_inputs(C, nh, nkv, hd, L, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(C, nh, hd, generator=g)
+    kc = torch.randn(L + 8, nkv, hd, generator=g).half()
+    vc = torch.randn(L + 8, nkv, hd, generator=g).half()
+    return q, kc, vc
+
+
+def test_attention_single_valid_key_returns_that_value_row():
+    """pos = 0: softmax over one key is exactly 1 and every masked weight exactly 0, so each query head
+    returns V[0] of its KV head, h // g (GQA grouping), bit for bit."""
+    nh, nkv, hd, L = 6, 2, 16, 32
+    q, kc, vc = _attn_inputs(1, nh, nkv, hd, L, 1)
+    allowed = torch.arange(L)[None, :] <= 0
+    o = R.attention(q, kc, vc, allowed, L, 1 / math.sqrt(hd)).reshape(nh, hd)
+    for h in range(nh):
+        assert torch.equal(o[h], vc[0, h // (nh // nkv)].float())
+
+
+def test_attention_equal_keys_give_mean_of_values():
+    """Equal keys give equal scores, so the weights are uniform over the valid keys: o is the mean of
+    V[0..pos] of the head's KV group."""
+    nh, nkv, hd, L, pos = 4, 2, 32, 64, 40
+    q, kc, vc = _attn_inputs(1, nh, nkv, hd, L, 2)
+    kc[:] = kc[0:1]
+    allowed = torch.arange(L)[None, :] <= pos
+    o = R.attention(q, kc, vc, allowed, L, 1 / math.sqrt(hd)).reshape(nh, hd)
+    for h in range(nh):
+        ref = vc[:pos + 1, h // 2].double().mean(0)
+        assert (o[h].double() - ref).abs().max().item() < 1e-6
+
+
+def test_attention_two_keys_sigmoid_pins_scale():
+    """Two valid keys with scores s0 = a * scale and s1 = 0 give weights sigmoid(a * scale) and its
+    complement: a dropped or doubled 1/sqrt(hd) fails this."""
+    hd, L = 64, 16
+    q = torch.zeros(1, 1, hd)
+    q[0, 0, 0] = 3.0
+    kc = torch.zeros(L, 1, hd, dtype=torch.float16)
+    vc = torch.zeros(L, 1, hd, dtype=torch.float16)
+    kc[0, 0, 0] = 1.0
+    vc[0, 0, :] = 1.0
+    vc[1, 0, :] = -1.0
+    allowed = torch.arange(L)[None, :] <= 1
+    scale = 1 / math.sqrt(hd)
+    o = R.attention(q, kc, vc, allowed, L, scale)
+    p0 = 1 / (1 + math.exp(-3.0 * scale))
+    assert abs(o[0, 0].item() - (p0 - (1 - p0))) < 1e-6
+
+
+def test_attention_ignores_rows_past_pos_and_bucket():
+    """Rows past pos (and past L) never change the output: filling them with large values gives the
+    identical result, which also equals an fp64 brute force over the valid rows. Checked for a causal
+    prefill chunk (row i sees keys <= start + i) with g = 3."""
+    C, nh, nkv, hd, L, start = 5, 6, 2, 32, 48, 20
+    q, kc, vc = _attn_inputs(C, nh, nkv, hd, L, 3)
+    pos = start + torch.arange(C)
+    allowed = torch.arange(L)[None, :] <= pos[:, None]
+    o = R.attention(q, kc, vc, allowed, L, 1 / math.sqrt(hd))
+    kc2, vc2 = kc.clone(), vc.clone()
+    kc2[start + C:] = 300.0
+    vc2[start + C:] = -500.0
+    assert torch.equal(R.attention(q, kc2, vc2, allowed, L, 1 / math.sqrt(hd)), o)
+    o = o.reshape(C, nh, hd).double()
+    for i in range(C):
+        n = start + i + 1
+        for h in range(nh):
+            kv = h // 3
+            s = (kc[:n, kv].double() @ q[i, h].double()) / math.sqrt(hd)
+            p = torch.softmax(s, 0)
+            ref = p @ vc[:n, kv].double()
+            assert (o[i, h] - ref).abs().max().item() < 1e-5
+
+
 # ------------------------------------------------------------------------------------------------
 # Whole step vs transformers (scripts/llm/test_tiny.py protocol)
 # ------------------------------------------------------------------------------------------------
