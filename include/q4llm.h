@@ -54,6 +54,39 @@ int q4llm_last_hip_error(void);
 /* ABI version of this header: bumped when a signature changes. */
 int q4llm_abi_version(void);
 
+/* Kernel-choice overrides, for tests and tuning sweeps only; no counterpart in the reference
+ * (whose kernels come from IREE's compiler). With no override set, every entry point picks its
+ * kernels by its fixed shape rule, and nothing in the library reads the process environment.
+ * An override takes effect for calls made after it returns (a HIP graph keeps the kernels it was
+ * captured with). The store is process-wide: callers that change it while another thread launches
+ * get either choice for that launch. */
+enum {
+  Q4_DBG_ATTN_S = 0,              /* decode attention keys per split: 32, 64 or 128 */
+  Q4_DBG_ATTN_PS = 1,             /* prefill attention keys per split: a multiple of 32, <= 512 */
+  Q4_DBG_ATTN_GENERIC = 2,        /* nonzero: every attention call on the generic split kernel */
+  Q4_DBG_ATTN_COMBINE_WG = 3,     /* nonzero: prefill attention merges with the workgroup combine */
+  Q4_DBG_GEMM_TILE = 4,           /* gemm_f16_nt tile entry (q4_config_info "gemm" index) */
+  Q4_DBG_GEMM_SPLIT = 5,          /* gemm_f16_nt_ws K split count */
+  Q4_DBG_GEMV_CFG = 6,            /* q4_gemv VALU entry */
+  Q4_DBG_MX_CFG = 7,              /* matrix-core GEMV entry */
+  Q4_DBG_GEMV_NO_MX = 8,          /* nonzero: fp32-x GEMVs on the reference layout stay on the VALU kernel */
+  Q4_DBG_MX_GRID = 9,             /* workgroup cap of the grid-stride matrix-core GEMV entries */
+  Q4_DBG_PREFILL_REF_LAYOUT = 10, /* nonzero: prefill projections read the reference layout, not T16 */
+  Q4_DBG_LINEAR_TILE = 11,        /* q4_linear_ws tile entry (then no K split and no fused SwiGLU) */
+  Q4_DBG_SWIGLU_UNFUSED = 12,     /* nonzero: prefill gate/up GEMM and SwiGLU as separate kernels */
+  Q4_DBG_NO_T16 = 13,             /* nonzero: q4llm_step's decode GEMVs read the reference layout */
+  Q4_DBG_REDUCE_SPLITS = 14,      /* nonzero: q4llm_step's K-split prefill projections add their partials
+                                     with the reduce kernel instead of leaving them to the next kernel */
+  Q4_DBG_COUNT = 15
+};
+#define Q4_DBG_UNSET (-2147483647 - 1)
+/* Sets override `key` to `value` (Q4_DBG_UNSET clears it). Q4_ERR_RANGE for an unknown key. */
+int q4_debug_override(int key, int value);
+/* The current value of override `key` (Q4_DBG_UNSET when not set) in *value. */
+int q4_debug_override_get(int key, int* value);
+/* Clears every override. */
+void q4_debug_clear(void);
+
 /* ---------------------------------------------------------------------------------------------
  * int4 weight format (reference: scripts/llm/llama_q4.py)
  * ------------------------------------------------------------------------------------------- */
@@ -356,7 +389,7 @@ int q4_gemv_cfg(const int32_t* qweight, const uint16_t* scales, const void* x, i
                 int y_dtype, const float* residual, int64_t N, int64_t K, int group, int cfg, int grid,
                 void* stream);
 int gemm_f16_num_configs(void);
-/* Number of q4_linear_ws tile entries (Q4_LINEAR_CFG selects one for sweeps and tests). */
+/* Number of q4_linear_ws tile entries (the Q4_DBG_LINEAR_TILE override selects one for sweeps and tests). */
 int q4_linear_ws_num_configs(void);
 int gemm_f16_nt_cfg(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K,
                     int64_t lda, int64_t ldb, int64_t ldc, int cfg, int split, void* stream);

@@ -44,14 +44,14 @@ AttnPlan plan_for(int C, int n_q, int n_kv, int L) {
   if (C == 1) {
     p.CB = 1;
     p.S = L <= 1024 ? 32 : (L <= 2048 ? 64 : 128);
-    const char* ov = getenv("Q4_ATTN_S");  // sweep override: keys per split (32, 64 or 128)
-    if (ov && (atoi(ov) == 32 || atoi(ov) == 64 || atoi(ov) == 128)) p.S = atoi(ov);
-  } else if (g <= kMfmaMaxG && getenv("Q4_ATTN_GENERIC") == nullptr) {
+    const int ov = debug_override(Q4_DBG_ATTN_S);  // sweep override: keys per split (32, 64 or 128)
+    if (ov == 32 || ov == 64 || ov == 128) p.S = ov;
+  } else if (g <= kMfmaMaxG && !debug_flag(Q4_DBG_ATTN_GENERIC)) {
     p.mfma = true;
     p.CB = 32;
     p.S = L <= 256 ? 64 : 128;
-    const char* ov = getenv("Q4_ATTN_PS");  // sweep override: keys per split (a multiple of 32, <= 512)
-    if (ov && atoi(ov) >= 32 && atoi(ov) <= 512 && atoi(ov) % 32 == 0) p.S = atoi(ov);
+    const int ov = debug_override(Q4_DBG_ATTN_PS);  // sweep override: keys per split (a multiple of 32, <= 512)
+    if (ov != Q4_DBG_UNSET && ov >= 32 && ov <= 512 && ov % 32 == 0) p.S = ov;
   } else {
     p.CB = kMaxQ / g < C ? kMaxQ / g : C;
     p.S = 64;
@@ -690,7 +690,7 @@ int launch_decode2(int g, const float* q, const uint16_t* kc, const uint16_t* vc
 // The register-resident decode path covers group sizes 1, 2, 3, 4, 8 and at most 64 splits.
 bool decode_fast(int C, int n_q, int n_kv, const AttnPlan& p) {
   const int g = n_q / n_kv;
-  return C == 1 && p.n_splits <= kDecodeMaxSplits && (g <= 4 || g == 8) && getenv("Q4_ATTN_GENERIC") == nullptr;
+  return C == 1 && p.n_splits <= kDecodeMaxSplits && (g <= 4 || g == 8) && !debug_flag(Q4_DBG_ATTN_GENERIC);
 }
 
 int launch_decode(const AttnPlan& p, int hd, int g, const float* q, const uint16_t* kc, const uint16_t* vc,
@@ -994,7 +994,7 @@ int attn_bucket_impl(const float* q, int q_row_stride, const uint16_t* k_cache, 
   if (rc) return rc;
   const int64_t rows = static_cast<int64_t>(C) * n_q;
   if (rows * p.n_splits * hd * 4 < (int64_t{1} << 31) && (!xh || (aligned(xh, 16) && aligned(xl, 16))) &&
-      (xh || aligned(out, 16)) && !getenv("Q4_ATTN_COMBINE_WG")) {
+      (xh || aligned(out, 16)) && !debug_flag(Q4_DBG_ATTN_COMBINE_WG)) {
     const unsigned blocks = static_cast<unsigned>((rows * (hd / 8) + 255) / 256);
     if (hd == 128)
       hipLaunchKernelGGL(attn_combine8_kernel<128>, dim3(blocks), dim3(256), 0, st, ws_ml, ws_o, out, rows, n_q,

@@ -25,6 +25,7 @@
 // the hardware consumes the k elements of a lane. Accumulator j of lane l holds
 // (row 8 * (j / 4) + 4 * (l / 32) + j % 4, col l % 32).
 #include "q4_common.h"
+#include "q4_internal.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -438,7 +439,7 @@ struct TileCfg {
   int bm, bn, wgm, wgn, nst, bk;
   bool sp = false;  // software-pipelined substeps (gemm_f16_nt_kernel<..., true>)
 };
-// Explicit CDNA4 tile list (index stable for gemm_f16_nt_cfg / Q4_GEMM_CFG).
+// Explicit CDNA4 tile list (index stable for gemm_f16_nt_cfg / the Q4_DBG_GEMM_TILE override).
 constexpr TileCfg kTiles[] = {
     {256, 256, 2, 4, 2, 64},        // 0: 8 waves of 128x64, 2 stages of K 64 (128 KB LDS)
     {128, 128, 2, 2, 2, 64},        // 1: 4 waves of 64x64, 2 stages (64 KB, two workgroups per CU)
@@ -491,11 +492,8 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // 128x128 entries, and a ping-pong schedule of two 4-wave groups on 256x256: each equal or slower on
 // every config-3 shape.
 int choose_tile(int64_t M, int64_t N, bool split_ok) {
-  const char* ov = getenv("Q4_GEMM_CFG");
-  if (ov && *ov) {
-    const int i = atoi(ov);
-    if (i >= 0 && i < kNumTiles) return i;
-  }
+  const int ov = debug_override(Q4_DBG_GEMM_TILE);
+  if (ov >= 0 && ov < kNumTiles) return ov;
   auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
   if (M >= 512) return tiles(0) >= 256 ? 0 : (tiles(6) >= 240 && tiles(6) <= 256 ? 6 : 1);
   if (split_ok && N % 4 == 0) return 2;
@@ -513,7 +511,7 @@ int choose_tile(int64_t M, int64_t N, bool split_ok) {
 // K split of tile entry ti: n_split K ranges of nk_split K steps each (the last may be shorter, none
 // empty); {1, 0} for no split. Only when N % 4 == 0 (the reduce kernel's four-column rows): M < 512
 // takes the split that brings the workgroups closest to 256 without exceeding it, each range at least
-// four K steps. Q4_GEMM_SPLIT forces a split count for sweeps.
+// four K steps. The Q4_DBG_GEMM_SPLIT override forces a split count for sweeps.
 struct GemmSplit {
   int n_split, nk_split;
 };
@@ -524,8 +522,7 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int ti) {
   const int nk = static_cast<int>(cdiv(K, t.bk));
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   int want = M < 512 ? static_cast<int>(std::min<int64_t>(256 / tiles, nk / 4)) : 1;
-  const char* ov = getenv("Q4_GEMM_SPLIT");
-  if (ov && *ov) want = atoi(ov);
+  if (debug_set(Q4_DBG_GEMM_SPLIT)) want = debug_override(Q4_DBG_GEMM_SPLIT);
   if (want <= 1 || nk < 2) return p;
   const int nk_s = static_cast<int>(cdiv(nk, std::min(want, nk)));
   const int S = static_cast<int>(cdiv(nk, nk_s));

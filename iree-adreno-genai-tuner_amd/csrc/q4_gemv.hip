@@ -577,7 +577,7 @@ struct Cfg {
   bool multi;
 };
 
-// The instantiated tile list (index stable: Q4_GEMV_CFG and q4_gemv_cfg select entries by index).
+// The instantiated tile list (index stable: the Q4_DBG_GEMV_CFG override and q4_gemv_cfg select entries by index).
 // Single-item entries need lpr * cpl >= K/32; every entry needs K/8 <= xw * 64 * waves.
 constexpr Cfg kCfgs[] = {
     {32, 3, 2, 5, 2, false},   // 0: K<=3072, 20 rows/WG (N=5120 -> 256 WGs)
@@ -654,11 +654,8 @@ bool cfg_fits(const Cfg& c, int64_t N, int64_t K) {
 // (the paired-row epilogues) restricts the choice to single-item entries with two rows per lane.
 int choose_cfg(int64_t N, int64_t K, bool paired) {
   auto usable = [&](int i) { return cfg_fits(kCfgs[i], N, K) && (!paired || (kCfgs[i].r == 2 && !kCfgs[i].multi)); };
-  const char* ov = getenv("Q4_GEMV_CFG");
-  if (ov && *ov) {
-    const int i = atoi(ov);
-    if (i >= 0 && i < kNumCfgs && usable(i)) return i;
-  }
+  const int ov = debug_override(Q4_DBG_GEMV_CFG);
+  if (ov >= 0 && ov < kNumCfgs && usable(ov)) return ov;
   if (paired) {
     if (K == 3072 && N == 5120) return 0;
     if (K == 3072 && N == 16384) return 6;

@@ -596,7 +596,7 @@ __global__ __launch_bounds__(RBW * WPB * 64) void q4_gemv_mx_kernel(
 using MxFn = void (*)(const int32_t*, const uint16_t*, const float*, const float*, float, float*, const float*, int, int,
                       int, int, MxEpi);
 
-// Explicit launch-shape list (index stable: Q4_MX_CFG selects an entry): row blocks per workgroup,
+// Explicit launch-shape list (index stable: the Q4_DBG_MX_CFG override selects an entry): row blocks per workgroup,
 // waves per row block, largest tiles per wave, used rows per 16-row block, grid-stride, and the
 // s_sleep of the weight-only and of the x waves before their first weight loads.
 struct MxCfg {
@@ -685,11 +685,8 @@ bool mx_fits(const MxCfg& c, int n_tiles, int nblk) {
 // Returns -1 when the VALU kernel should run.
 int mx_choose(int n_tiles, int nblk, int64_t n_rb16, bool pair, bool tiled) {
   auto fits = [&](int i) { return mx_fits(kMxCfgs[i], n_tiles, nblk) && (!pair || kMxCfgs[i].rpb == 16); };
-  const char* ov = getenv("Q4_MX_CFG");
-  if (ov && *ov) {
-    const int i = atoi(ov);
-    if (i >= 0 && i < kNumMxCfgs && fits(i)) return i;
-  }
+  const int ov = debug_override(Q4_DBG_MX_CFG);
+  if (ov >= 0 && ov < kNumMxCfgs && fits(ov)) return ov;
   if (n_tiles == 6 && pair) return n_rb16 <= 512 ? 11 : 8;
   if (n_tiles == 6 && !pair && n_rb16 > 4096) return 19;
   // the 3072x3072 o-projection: the VALU kernel on the reference layout (3.25 us) beats the matrix
@@ -740,7 +737,7 @@ bool gemv_mx_takes_t16(int64_t N, int64_t K, int group, bool pair) {
 int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* x, const float* aux, float eps, float* y,
                    const float* residual, int64_t N, int64_t K, int group, int prologue, int epilogue,
                    const GemvEpi* ep, hipStream_t stream, bool tiled, int* grid_out) {
-  if (!tiled && getenv("Q4_GEMV_NO_MX")) return Q4_ERR_UNSUPPORTED;
+  if (!tiled && debug_flag(Q4_DBG_GEMV_NO_MX)) return Q4_ERR_UNSUPPORTED;
   if (K % 32 || K > 16384 || N <= 0) return Q4_ERR_UNSUPPORTED;
   if (group != 32 && group != 128) return Q4_ERR_UNSUPPORTED;
   if (K % group) return Q4_ERR_UNSUPPORTED;
@@ -778,8 +775,8 @@ int gemv_mx_launch(const int32_t* qweight, const uint16_t* scales, const float* 
   const int64_t n_wg = (n_rb + c.rbw - 1) / c.rbw;
   int64_t grid = n_wg;
   if (c.multi) {
-    const char* gv = getenv("Q4_MX_GRID");
-    const int64_t cap = gv && atoi(gv) > 0 ? atoi(gv) : 1024;
+    const int gv = debug_override(Q4_DBG_MX_GRID);
+    const int64_t cap = gv != Q4_DBG_UNSET && gv > 0 ? gv : 1024;
     grid = n_wg < cap ? n_wg : cap;
   }
   if (ea.amax && grid > ep->amax_cap) return Q4_ERR_WORKSPACE;

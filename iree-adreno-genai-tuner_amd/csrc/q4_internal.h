@@ -5,12 +5,24 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
 #include "q4llm.h"
 
 namespace q4 {
+
+// Kernel-choice overrides set through q4_debug_override (q4_status.cpp): Q4_DBG_UNSET when the key
+// is not set. The launch paths consult these instead of the process environment.
+extern std::atomic<int> g_debug[Q4_DBG_COUNT];
+inline int debug_override(int key) { return g_debug[key].load(std::memory_order_relaxed) ^ Q4_DBG_UNSET; }
+inline bool debug_set(int key) { return debug_override(key) != Q4_DBG_UNSET; }
+// a flag override: set and nonzero
+inline bool debug_flag(int key) {
+  const int v = debug_override(key);
+  return v != Q4_DBG_UNSET && v != 0;
+}
 
 // (value, index) of a running argmax: the first index of the maximum, a NaN counting as larger than
 // every number (torch.argmax, llama_q4.py:239).

@@ -877,7 +877,7 @@ struct LinWsTile {
   int bm, bn, wm, wn, nst, ks;
   bool pipe;
 };
-// Explicit tile list (index stable for Q4_LINEAR_CFG sweeps): the entries the rules below pick. Swept
+// Explicit tile list (index stable for Q4_DBG_LINEAR_TILE sweeps): the entries the rules below pick. Swept
 // and removed (slower on every 3B prefill shape at M = 128, 256 and 1024): 4-wave 64x64, 32x64 and
 // 64x128 wave tiles on 128x128, 64x128, 128x64 and 64x256, 32x128 wave tiles (4 or 8 waves on 64x256,
 // 128x128, 128x256, 64x512), 64x64 waves on 128x256, k-split 2-wave and 64x64 / 128x64 / 32x96 /
@@ -912,9 +912,9 @@ constexpr size_t kLinWsLds[] = {lin_ws_lds<0>(), lin_ws_lds<1>(), lin_ws_lds<2>(
 static_assert(kLinWsTiles[kSplitTile].pipe && kLinWsTiles[kSplitTile].ks == 1, "the T16 variants need the pipelined loop");
 
 // A T16 source the K-split tile can read: both pointers, a group the layout takes, whole 16-row tiles
-// for the paired orders, 16-byte aligned tiles (Q4_PREFILL_REF_LAYOUT set: the reference layout).
+// for the paired orders, 16-byte aligned tiles (Q4_DBG_PREFILL_REF_LAYOUT set: the reference layout).
 bool t16_usable(const T16Src* t, int64_t N, int group, int pairing_needed) {
-  if (!t || !t->tiles || !t->scales || getenv("Q4_PREFILL_REF_LAYOUT")) return false;
+  if (!t || !t->tiles || !t->scales || debug_flag(Q4_DBG_PREFILL_REF_LAYOUT)) return false;
   if ((group != 32 && group != 128) || !aligned(t->tiles, 16) || !aligned(t->scales, 4)) return false;
   if (pairing_needed >= 0 && t->pairing != pairing_needed) return false;
   if (t->pairing == Q4_PAIR_SWIGLU) return N % 16 == 0;
@@ -1005,7 +1005,7 @@ size_t linear_split_part_bytes(int64_t M, int64_t N, int64_t K, int group) {
 // M = 128, 256 and 1024 (graph replays on one MI355X): with a partial buffer `part` of at least
 // linear_split_part_bytes, the K-split 64x256 tile where linear_split_plan gives a split (every M <= 256
 // chunk of the 3072-, 5120- and 8192-wide projections), then linear_reduce_kernel; otherwise the 32x64
-// k-split tile while it gives at most 768 workgroups, else 64x64. Q4_LINEAR_CFG overrides (no K split).
+// k-split tile while it gives at most 768 workgroups, else 64x64. Q4_DBG_LINEAR_TILE overrides (no K split).
 int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const int32_t* qw, const uint16_t* sc,
                      float* y, const float* res, int64_t N, int64_t K, int group, hipStream_t st, float* part,
                      size_t part_bytes, int* deferred, const T16Src* t16) {
@@ -1013,8 +1013,8 @@ int q4_linear_planes(const uint16_t* xh, const uint16_t* xl, int64_t M, const in
   if (!y) return Q4_ERR_NULL;
   if (deferred) *deferred = 0;
   int ti = -1;
-  const char* ov = getenv("Q4_LINEAR_CFG");
-  if (ov && *ov && atoi(ov) >= 0 && atoi(ov) < kNumLinWs) ti = atoi(ov);
+  const int ov = debug_override(Q4_DBG_LINEAR_TILE);
+  if (ov >= 0 && ov < kNumLinWs) ti = ov;
   const LinearSplit sp = linear_split_plan(M, N, K, group);
   if (ti < 0 && part && sp.n_split > 1 && part_bytes >= linear_split_part_bytes(M, N, K, group) &&
       (M * N) % 4 == 0 && aligned(part, 16) && aligned(y, 16) && (!res || aligned(res, 16)) &&
@@ -1076,8 +1076,7 @@ int q4_linear_planes_swiglu(const uint16_t* xh, const uint16_t* xl, int64_t M, c
                             const T16Src* t16) {
   if (int e = planes_args(xh, xl, M, qw, sc, N, K, group)) return e;
   if (!oh || !ol) return Q4_ERR_NULL;
-  const char* ov = getenv("Q4_LINEAR_CFG");
-  if ((ov && *ov) || getenv("Q4_SWIGLU_UNFUSED")) return Q4_ERR_UNSUPPORTED;
+  if (debug_set(Q4_DBG_LINEAR_TILE) || debug_flag(Q4_DBG_SWIGLU_UNFUSED)) return Q4_ERR_UNSUPPORTED;
   constexpr LinWsTile t = kLinWsTiles[kSplitTile];
   const int64_t wide = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   if (!(M <= 256 && wide >= 256) || N % t.bn || (N / 2) % 32 || ol != oh + M * (N / 2)) return Q4_ERR_UNSUPPORTED;

@@ -192,8 +192,8 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   uint16_t* xh = static_cast<uint16_t*>(lin_ws);
   uint16_t* xl = xh + static_cast<size_t>(C) * kmax;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  // decode GEMVs on the T16 copies where the model has them (Q4_NO_T16 set: the reference layout)
-  const bool use_t16 = fused && !getenv("Q4_NO_T16");
+  // decode GEMVs on the T16 copies where the model has them (Q4_DBG_NO_T16 set: the reference layout)
+  const bool use_t16 = fused && !q4::debug_flag(Q4_DBG_NO_T16);
   auto has = [&](const q4llm_t16& t) { return use_t16 && t.tiles && t.scales; };
   // prefill projections on the 64x256 tile read the same T16 copies (fewer cache lines per load)
   auto src = [&](const q4llm_t16& t, int pairing) {
@@ -202,7 +202,9 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
   Q4_TRY(q4_embed_lookup(m->embed_q, m->embed_s, tokens, h, C, m->vocab, D, m->group, stream));
   // K-split partials left by the last prefill projection for the kernel after it to add (0: none)
   int pending = 0;
-  const bool defer_norm = planes && q4::rmsnorm_takes_partials(D);
+  // (Q4_DBG_REDUCE_SPLITS set: every K split is reduced by its projection's own reduce kernel)
+  const bool reduce_splits = q4::debug_flag(Q4_DBG_REDUCE_SPLITS);
+  const bool defer_norm = planes && q4::rmsnorm_takes_partials(D) && !reduce_splits;
   for (int i = 0; i < m->n_layers; ++i) {
     const q4llm_layer& ly = m->layers[i];
     uint16_t* kc = static_cast<uint16_t*>(caches[2 * i]);
@@ -219,7 +221,7 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
       Q4_TRY(q4::rmsnorm_planes(h, ly.ln_in, xh, xl, C, D, m->eps, st, part, pending));
       pending = 0;
       // the qkv partials are added by the RoPE + KV-write kernel
-      const bool defer_rope = q4::rope_kv_takes_partials(qkv, m->cos_t, m->sin_t, kc, vc, hd);
+      const bool defer_rope = q4::rope_kv_takes_partials(qkv, m->cos_t, m->sin_t, kc, vc, hd) && !reduce_splits;
       int qkv_split = 0;
       const q4::T16Src qkv_t = src(ly.wqkv_t, Q4_PAIR_ROPE);
       Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wqkv_q, ly.wqkv_s, qkv, nullptr, qkv_w, D, m->group, st, part,
@@ -277,11 +279,12 @@ int step_impl(const q4llm_model* m, const int32_t* tokens, int C, const int32_t*
                                     lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));
       } else {
         if (fused != Q4_ERR_UNSUPPORTED) return fused;
-        // a K split of gate/up is added by the silu_mul kernel (Q4_SWIGLU_UNFUSED set: by its own
+        // a K split of gate/up is added by the silu_mul kernel (Q4_DBG_SWIGLU_UNFUSED set: by its own
         // reduce kernel first); same sums, same order
         int gu_split = 0;
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wgu_q, ly.wgu_s, gu, nullptr, 2 * m->inter, D, m->group, st, part,
-                                    lo.part_bytes, getenv("Q4_SWIGLU_UNFUSED") ? nullptr : &gu_split, &wgu_t));
+                                    lo.part_bytes, q4::debug_flag(Q4_DBG_SWIGLU_UNFUSED) || reduce_splits ? nullptr : &gu_split,
+                                    &wgu_t));
         Q4_TRY(q4::silu_mul_planes(gu, xh, xl, C, m->inter, st, part, gu_split));
         Q4_TRY(q4::q4_linear_planes(xh, xl, C, ly.wdown_q, ly.wdown_s, h, h, D, m->inter, m->group, st, part,
                                     lo.part_bytes, defer_norm ? &pending : nullptr, &wdown_t));

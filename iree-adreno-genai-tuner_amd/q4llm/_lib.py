@@ -27,6 +27,9 @@ SIGNATURES = {
     "q4llm_status_string": [i32],
     "q4llm_last_hip_error": [],
     "q4llm_abi_version": [],
+    "q4_debug_override": [i32, i32],
+    "q4_debug_override_get": [i32, C.POINTER(i32)],
+    "q4_debug_clear": [],
     "q4_quantize": [p, p, p, i64, i64, i32, p],
     "q4_unpack": [p, p, i64, i64, p],
     "q4_dequant": [p, p, p, i32, i64, i64, i32, p],
@@ -70,7 +73,7 @@ SIGNATURES = {
     "q4_probe_empty": [i32, i32, p],
     "q4_probe_wait": [i64, p],
 }
-_RESTYPES = {"q4llm_status_string": C.c_char_p}
+_RESTYPES = {"q4llm_status_string": C.c_char_p, "q4_debug_clear": None}
 
 
 class Q4Error(RuntimeError):

@@ -370,3 +370,31 @@ def q4_gemv_t16(tiles, tile_scales, x, N, K, group, norm_w=None, eps=1e-5, epilo
     LIB.call("q4_gemv_t16", ptr(tiles), ptr(tile_scales), ptr(x), pro, ptr(norm_w), eps, epilogue,
              None if rope is None else C.addressof(rope), ptr(out), ptr(residual), N, K, group, stream_of(x.device))
     return out
+
+
+# ------------------------------------------------------------------------------------------------
+# Kernel-choice overrides (tests and tuning sweeps; include/q4llm.h q4_debug_override)
+# ------------------------------------------------------------------------------------------------
+
+DEBUG_KEYS = {
+    "attn_s": 0, "attn_ps": 1, "attn_generic": 2, "attn_combine_wg": 3, "gemm_tile": 4, "gemm_split": 5,
+    "gemv_cfg": 6, "mx_cfg": 7, "gemv_no_mx": 8, "mx_grid": 9, "prefill_ref_layout": 10, "linear_tile": 11,
+    "swiglu_unfused": 12, "no_t16": 13, "reduce_splits": 14,
+}
+DEBUG_UNSET = -(1 << 31)
+
+
+def debug_override(name: str, value=None) -> None:
+    """Force a kernel choice for later calls (value an int; None clears it). Names: DEBUG_KEYS. With
+    none set the library follows its fixed rules and reads no environment variables."""
+    LIB.call("q4_debug_override", DEBUG_KEYS[name], DEBUG_UNSET if value is None else int(value))
+
+
+def debug_override_get(name: str):
+    v = C.c_int(0)
+    LIB.call("q4_debug_override_get", DEBUG_KEYS[name], C.byref(v))
+    return None if v.value == DEBUG_UNSET else v.value
+
+
+def debug_clear() -> None:
+    LIB.load().q4_debug_clear()

@@ -37,3 +37,14 @@ def _announce(request):
     if request.node.get_closest_marker("gpu") is not None:
         print(f"\n[gpu-test] {request.node.nodeid}", flush=True)
     yield
+
+
+@pytest.fixture
+def kernel_override():
+    """Sets library kernel-choice overrides (q4llm.ops.debug_override) for one test and clears every
+    override afterwards, pass or fail: kernel_override("attn_generic", 1), kernel_override("x", None)."""
+    from q4llm import ops
+    try:
+        yield ops.debug_override
+    finally:
+        ops.debug_clear()

@@ -92,3 +92,28 @@ def test_python_wrapper_raises_typed_error():
     with pytest.raises(Q4Error) as ei:
         LIB.call("q4_unpack", FAKE, FAKE, 4, 12, None)
     assert ei.value.status == ERR["SHAPE"]
+
+
+def test_debug_overrides_roundtrip_and_no_environment_reads():
+    """Kernel-choice overrides are explicit calls (q4_debug_override): unset by default, set, read back
+    and cleared; an unknown key is Q4_ERR_RANGE. The built library imports no getenv, so no process
+    environment variable can change which kernels the default path runs."""
+    import shutil
+    import subprocess
+    from q4llm import ops
+    ops.debug_clear()
+    assert all(ops.debug_override_get(k) is None for k in ops.DEBUG_KEYS)
+    ops.debug_override("mx_cfg", 0)
+    ops.debug_override("attn_s", 64)
+    assert ops.debug_override_get("mx_cfg") == 0 and ops.debug_override_get("attn_s") == 64
+    ops.debug_override("attn_s", None)
+    assert ops.debug_override_get("attn_s") is None and ops.debug_override_get("mx_cfg") == 0
+    ops.debug_clear()
+    assert ops.debug_override_get("mx_cfg") is None
+    f = LIB.raw("q4_debug_override")
+    assert f(len(ops.DEBUG_KEYS), 1) == ERR["RANGE"] and f(-1, 1) == ERR["RANGE"]
+    nm = shutil.which("nm")
+    if nm:
+        undef = subprocess.run([nm, "-D", "--undefined-only", str(LIB_PATH)], capture_output=True, text=True,
+                               check=True).stdout
+        assert "getenv" not in undef and "secure_getenv" not in undef

@@ -7,9 +7,8 @@ The products are exact, so the result must sit within fp32 accumulation error of
 conversion could get wrong: groups spanning many orders of magnitude, all-zero groups, exact
 powers of two, a single non-zero element. The grid-stride variant (matrices taller than 65536 rows,
 the tied LM head) and the short-matrix variant (8 used rows per block) are covered, and the result
-is compared with the VALU kernel (Q4_GEMV_NO_MX) and checked to be deterministic."""
+is compared with the VALU kernel (the gemv_no_mx override) and checked to be deterministic."""
 
-import os
 
 import numpy as np
 import pytest
@@ -33,14 +32,14 @@ def _problem(n, k, group, seed, x=None):
 
 def _run(dev, qw, sc, x, group, no_mx=False):
     if no_mx:
-        os.environ["Q4_GEMV_NO_MX"] = "1"
+        ops.debug_override("gemv_no_mx", 1)
     try:
         y = torch.full((qw.shape[0],), float("nan"), device=dev)
         ops.q4_gemv(qw.to(dev), sc.to(dev), x.to(dev), group, out=y)
         torch.cuda.synchronize()
         return y.cpu().double()
     finally:
-        os.environ.pop("Q4_GEMV_NO_MX", None)
+        ops.debug_override("gemv_no_mx", None)
 
 
 def _rel(y, ref):

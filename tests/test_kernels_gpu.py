@@ -74,13 +74,13 @@ def test_attn_decode_edges(dev, start, L):
 @pytest.mark.parametrize("L,start", [(32, 7), (256, 200), (1024, 1023), (2048, 1100), (4096, 2049), (8192, 5000),
                                      (16384, 9000)])
 @pytest.mark.parametrize("path", ["fast", "generic"])
-def test_attn_decode_group_sizes(dev, monkeypatch, nq, nkv, hd, L, start, path):
+def test_attn_decode_group_sizes(dev, kernel_override, nq, nkv, hd, L, start, path):
     """Decode over group sizes 1-8 (the register-resident kernel takes g in {1, 2, 3, 4, 8} and up to 64
     splits; g = 5 and L = 16384 take the generic split kernel) and both head dims, each path forced."""
     if path == "generic":
-        monkeypatch.setenv("Q4_ATTN_GENERIC", "1")
+        kernel_override("attn_generic", 1)
     else:
-        monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
+        kernel_override("attn_generic", None)
     g = torch.Generator().manual_seed(nq * 7 + L + start)
     q = torch.randn(1, nq, hd, generator=g)
     kc = torch.randn(L, nkv, hd, generator=g).half()
@@ -98,17 +98,17 @@ def test_attn_decode_group_sizes(dev, monkeypatch, nq, nkv, hd, L, start, path):
                                                   (128, 128, 384, 32, 8, 64), (33, 0, 40, 40, 8, 128),
                                                   (48, 1900, 2048, 24, 8, 128)])
 @pytest.mark.parametrize("path", ["mfma", "generic", "mfma_wg_combine"])
-def test_attn_prefill_chunk(dev, monkeypatch, Cn, start, L, nq, nkv, hd, path):
+def test_attn_prefill_chunk(dev, kernel_override, Cn, start, L, nq, nkv, hd, path):
     """Prefill chunks on the matrix-core kernel (group sizes 1-8) and on the generic split kernel
     (forced; also the path for group sizes above 8): ragged C and L, start > 0, up to 16 key splits
     (past the 8 the combine loads up front); the splits merged by the per-thread combine kernel or
-    (Q4_ATTN_COMBINE_WG) by the workgroup-per-(row, head) one."""
-    monkeypatch.delenv("Q4_ATTN_GENERIC", raising=False)
-    monkeypatch.delenv("Q4_ATTN_COMBINE_WG", raising=False)
+    (the attn_combine_wg override) by the workgroup-per-(row, head) one."""
+    kernel_override("attn_generic", None)
+    kernel_override("attn_combine_wg", None)
     if path == "generic":
-        monkeypatch.setenv("Q4_ATTN_GENERIC", "1")
+        kernel_override("attn_generic", 1)
     elif path == "mfma_wg_combine":
-        monkeypatch.setenv("Q4_ATTN_COMBINE_WG", "1")
+        kernel_override("attn_combine_wg", 1)
     g = torch.Generator().manual_seed(Cn + start)
     qkv_w = (nq + 2 * nkv) * hd
     qkv = torch.randn(Cn, qkv_w, generator=g)
@@ -144,21 +144,17 @@ def test_gemm_config3(dev, M, N, K):
     assert err <= 1e-2 * rms, (err, rms)
 
 
-@pytest.mark.parametrize("sid,M,N,K", [("S1", 1024, 1024, 1024), ("S2", 128, 3072, 3072), ("S3", 4096, 64, 1024),
-                                        ("S4", 16, 4096, 4096), ("S5", 256, 256, 8192), ("S6", 2048, 2048, 32),
-                                        ("S7", 1, 4096, 4096), ("S8", 768, 768, 768)])
-def test_gemm_reference_nt_shapes_tol(dev, sid, M, N, K):
+@pytest.mark.parametrize("sid", [t[0] for t in synth.REF_GEMM_SHAPES])
+def test_gemm_reference_nt_shapes_tol(dev, sid):
     """All eight of the reference's problems with its own data recipe and TOL (gemm/shapes.py:41-66):
     U(-1,1) from default_rng(seed + id), max|C - Cref| / max|Cref| <= 5e-3. The kernel is NT; the NN,
     TN and TT problems (S1, S3, S5, S6, S8) run on their logical A [M,K] and B^T [N,K]."""
-    rng = np.random.default_rng(0 + int(sid[1:]))
-    a = rng.uniform(-1, 1, (M, K)).astype(np.float16)
-    b = rng.uniform(-1, 1, (K, N)).astype(np.float16)
+    a, b = synth.ref_gemm_problem(sid)
     cref = a.astype(np.float32) @ b.astype(np.float32)
     A = torch.from_numpy(a).to(dev)
     Bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(dev)  # stored transposed: [N, K]
     c = ops.gemm_f16_nt(A, Bt).float().cpu().numpy()
-    assert np.abs(c - cref).max() / np.abs(cref).max() <= 5e-3
+    assert np.abs(c - cref).max() / np.abs(cref).max() <= synth.REF_GEMM_TOL
 
 
 def test_gemm_all_tiles_and_ragged_edges(dev):
@@ -192,7 +188,7 @@ def test_gemm_ws_config3(dev, M, N, K):
     assert (c.cpu().float() - c2).abs().max().item() <= 1e-2 * rms
 
 
-def test_gemm_ws_forced_splits_every_tile(dev, monkeypatch):
+def test_gemm_ws_forced_splits_every_tile(dev, kernel_override):
     """Every tile entry with K split 2, 3 and 5 ways (ranges not a multiple of the stage count)
     at a ragged shape, and twice in a row into the same workspace: host fp32 reference each time."""
     from q4llm._lib import config_table
@@ -203,9 +199,9 @@ def test_gemm_ws_forced_splits_every_tile(dev, monkeypatch):
     bar = 1e-2 * ref.pow(2).mean().sqrt().item()
     ws = torch.empty(5 * M * N * 4, dtype=torch.uint8, device=dev)
     for cfg, info in enumerate(config_table("gemm")):
-        monkeypatch.setenv("Q4_GEMM_CFG", str(cfg))
+        kernel_override("gemm_tile", cfg)
         for S in (2, 3, 5):
-            monkeypatch.setenv("Q4_GEMM_SPLIT", str(S))
+            kernel_override("gemm_split", S)
             nk = -(-K // info[5])
             s_eff = -(-nk // -(-nk // S))  # ranges of ceil(nk / S) steps, none empty (5 -> 4 at 12 steps)
             assert ops.gemm_f16_nt_ws_bytes(M, N, K) == s_eff * M * N * 4
@@ -259,7 +255,7 @@ def test_q4_linear_fp32_accuracy(dev, M, N, K, group):
 @pytest.mark.parametrize("M,N,K,group", [(256, 5120, 3072, 128), (256, 3072, 8192, 128), (16, 1408, 256, 32),
                                          (16, 256, 704, 32), (7, 100, 128, 64), (300, 3072, 3072, 128),
                                          (256, 16384, 3072, 128), (33, 200, 320, 64), (20, 130, 192, 96)])
-def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch):
+def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, kernel_override):
     """The workspace entry point (x split into fp16 hi/lo planes, multi-stage pipeline) keeps the
     fp32-level accuracy of q4_linear on every tile of its list, with ragged M and N; a group that is not
     a power of two (96) takes the workspace-free kernel."""
@@ -273,7 +269,7 @@ def test_q4_linear_ws_fp32_accuracy_every_tile(dev, M, N, K, group, monkeypatch)
     xd, qd, sd = x.to(dev), qw.to(dev), sc.to(dev)
     from q4llm._lib import LIB
     for cfg in [""] + [str(i) for i in range(LIB.raw("q4_linear_ws_num_configs")())]:
-        monkeypatch.setenv("Q4_LINEAR_CFG", cfg)
+        kernel_override("linear_tile", int(cfg) if cfg else None)
         y = nan_like((M, N), torch.float32, dev)
         ops.q4_linear_ws(xd, qd, sd, group, out=y)
         assert (y.cpu().double() - ref).abs().max().item() <= 1e-5 * rms, cfg

@@ -138,10 +138,10 @@ def test_llama32_3b_generation_matches_golden(dev):
     torch.cuda.empty_cache()
 
 
-def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch):
+def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, kernel_override):
     """A 256-row chunk with intermediate 8192 takes the gate/up GEMM with the SwiGLU epilogue (planes of
     silu(gate) * up written by the GEMM): bit-identical logits and caches to the GEMM + silu_mul pair
-    (Q4_SWIGLU_UNFUSED), and the oracle's next token with logits within the per-op tolerance."""
+    (the swiglu_unfused override), and the oracle's next token with logits within the per-op tolerance."""
     cfg = dict(synth.TINY, intermediate_size=8192, num_hidden_layers=2)
     ours, ref = build_pair(cfg, 32, 256)
     prompt = synth.prompt_ids(256, cfg["vocab_size"], seed=3)
@@ -149,10 +149,10 @@ def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch
     start, last = torch.tensor([0], dtype=torch.int32), torch.tensor([255], dtype=torch.int32)
     c_fused = ours.new_caches()
     n_f, l_f = ours.step(toks, start, last, c_fused, 256)
-    monkeypatch.setenv("Q4_SWIGLU_UNFUSED", "1")
+    kernel_override("swiglu_unfused", 1)
     c_two = ours.new_caches()
     n_t, l_t = ours.step(toks, start, last, c_two, 256)
-    monkeypatch.delenv("Q4_SWIGLU_UNFUSED")
+    kernel_override("swiglu_unfused", None)
     assert torch.equal(l_f, l_t) and int(n_f.item()) == int(n_t.item())
     for a, b in zip(c_fused, c_two):
         assert torch.equal(a, b)
@@ -161,11 +161,11 @@ def test_prefill_swiglu_epilogue_matches_two_kernels_and_oracle(dev, monkeypatch
     assert (l_f.cpu() - r_l).abs().max().item() <= tol(r_l)
 
 
-def test_prefill_chunk128_k_split_paths_vs_oracle(dev, monkeypatch):
+def test_prefill_chunk128_k_split_paths_vs_oracle(dev, kernel_override):
     """A 128-row chunk takes every K-split path of the prefill step: qkv, o and down split and completed
     by the RoPE / rms_norm kernels after them, and gate/up (too few 64x256 tiles at 128 rows for its
     SwiGLU epilogue) split 2 ways, its partials added by the silu_mul kernel: bit-identical to adding
-    them with the reduce kernel first (Q4_SWIGLU_UNFUSED). Two chunks (the second reading the first's
+    them with the reduce kernel first (the swiglu_unfused override). Two chunks (the second reading the first's
     caches), next token and logits against the oracle."""
     cfg = dict(synth.TINY, intermediate_size=8192, num_hidden_layers=2)
     ours, ref = build_pair(cfg, 32, 256)
@@ -175,9 +175,9 @@ def test_prefill_chunk128_k_split_paths_vs_oracle(dev, monkeypatch):
         toks = torch.tensor([prompt[s0:s0 + 128]], dtype=torch.int32)
         start, last = torch.tensor([s0], dtype=torch.int32), torch.tensor([127], dtype=torch.int32)
         n_o, l_o = ours.step(toks, start, last, c_ours, 256)
-        monkeypatch.setenv("Q4_SWIGLU_UNFUSED", "1")
+        kernel_override("swiglu_unfused", 1)
         n_t, l_t = ours.step(toks, start, last, c_two, 256)
-        monkeypatch.delenv("Q4_SWIGLU_UNFUSED")
+        kernel_override("swiglu_unfused", None)
         assert torch.equal(l_o, l_t) and int(n_o.item()) == int(n_t.item()), s0
         for a, b in zip(c_ours, c_two):
             assert torch.equal(a, b), s0
@@ -186,11 +186,42 @@ def test_prefill_chunk128_k_split_paths_vs_oracle(dev, monkeypatch):
         assert (l_o.cpu() - r_l).abs().max().item() <= tol(r_l), s0
 
 
+@pytest.mark.parametrize("cfg_kw,chunk", [
+    # qkv and o: 4 partials each; down: 128 (past the 12 loaded with the row: the tail loop); gate/up: 2
+    (dict(intermediate_size=8192), 128),
+    # qkv 8 (RoPE kernel), o 4 and down 7 (rms_norm, 6-wide and 12-wide batches), gate/up 8 (silu_mul)
+    (dict(hidden_size=512, intermediate_size=448), 128),
+    (dict(hidden_size=512, intermediate_size=448), 256),
+])
+def test_prefill_deferred_partials_bit_identical_to_reduce_kernel(dev, kernel_override, cfg_kw, chunk):
+    """The kernels that add a K-split projection's partials themselves (RoPE + KV write after qkv,
+    rms_norm after o and down, silu_mul after a split gate/up, the final norm's selected row) give the
+    same bits as reducing each projection with linear_reduce_kernel first and running the plain
+    kernels (the reduce_splits override): logits, next token and every K/V cache, chunk after chunk."""
+    cfg = dict(synth.TINY, num_hidden_layers=2, **cfg_kw)
+    ours, ref = build_pair(cfg, 32, 256)
+    prompt = synth.prompt_ids(256, cfg["vocab_size"], seed=7)
+    c_def, c_red, c_ref = ours.new_caches(), ours.new_caches(), ref.new_caches()
+    for s0 in range(0, 256, chunk):
+        toks = torch.tensor([prompt[s0:s0 + chunk]], dtype=torch.int32)
+        start, last = torch.tensor([s0], dtype=torch.int32), torch.tensor([chunk - 1], dtype=torch.int32)
+        n_d, l_d = ours.step(toks, start, last, c_def, 256)
+        kernel_override("reduce_splits", 1)
+        n_r, l_r = ours.step(toks, start, last, c_red, 256)
+        kernel_override("reduce_splits", None)
+        assert torch.equal(l_d, l_r) and int(n_d.item()) == int(n_r.item()), s0
+        for a, b in zip(c_def, c_red):
+            assert torch.equal(a, b), s0
+        r_n, r_l = ref.step(toks, start, last, c_ref, 256)
+        assert int(n_d.item()) == int(r_n.item()), s0
+        assert (l_d.cpu() - r_l).abs().max().item() <= tol(r_l), s0
+
+
 @pytest.mark.parametrize("chunk", [256, 128])
-def test_prefill_t16_source_matches_reference_layout(dev, monkeypatch, chunk):
+def test_prefill_t16_source_matches_reference_layout(dev, kernel_override, chunk):
     """Prefill projections on the 64x256 tile read the decode T16 copies (RoPE-paired qkv, plain o and
     down, SwiGLU-paired gate/up) instead of the reference layout: the same sums in the same order, so
-    the logits and the K/V caches are bit-identical to Q4_PREFILL_REF_LAYOUT (256-row chunk: the SwiGLU
+    the logits and the K/V caches are bit-identical to the prefill_ref_layout override (256-row chunk: the SwiGLU
     epilogue; 128 rows: every projection K-split), and the token matches the oracle."""
     cfg = dict(synth.TINY, hidden_size=1024, num_attention_heads=8, num_key_value_heads=4, head_dim=128,
                intermediate_size=8192, num_hidden_layers=2)
@@ -201,10 +232,10 @@ def test_prefill_t16_source_matches_reference_layout(dev, monkeypatch, chunk):
     start, last = torch.tensor([0], dtype=torch.int32), torch.tensor([chunk - 1], dtype=torch.int32)
     c_t = ours.new_caches()
     n_t, l_t = ours.step(toks, start, last, c_t, 256)
-    monkeypatch.setenv("Q4_PREFILL_REF_LAYOUT", "1")
+    kernel_override("prefill_ref_layout", 1)
     c_r = ours.new_caches()
     n_r, l_r = ours.step(toks, start, last, c_r, 256)
-    monkeypatch.delenv("Q4_PREFILL_REF_LAYOUT")
+    kernel_override("prefill_ref_layout", None)
     assert torch.equal(l_t, l_r) and int(n_t.item()) == int(n_r.item())
     for a, b in zip(c_t, c_r):
         assert torch.equal(a, b)

@@ -94,8 +94,8 @@ def mx_entries(k, group, pair):
 
 @pytest.mark.parametrize("n,k,group", [(3072, 3072, 128), (3072, 8192, 128), (128256 // 8, 3072, 128),
                                        (1000, 3072, 128), (256, 704, 32), (1024, 256, 32), (37, 256, 32)])
-def test_plain_and_norm_bit_identical_on_every_entry(dev, n, k, group, monkeypatch):
-    """Each launch entry that takes the shape (forced with Q4_MX_CFG on both layouts)."""
+def test_plain_and_norm_bit_identical_on_every_entry(dev, n, k, group, kernel_override):
+    """Each launch entry that takes the shape (forced with the mx_cfg override on both layouts)."""
     from q4llm._lib import LIB, ptr, stream_of
     qw, sc = weights(dev, n, k, group, n)
     tp = ops.t16_pack(qw, sc, group)
@@ -107,14 +107,14 @@ def test_plain_and_norm_bit_identical_on_every_entry(dev, n, k, group, monkeypat
     assert entries
     for cfg in entries:
         print(f"[t16] {n}x{k} g{group} entry {cfg}", flush=True)
-        monkeypatch.setenv("Q4_MX_CFG", str(cfg))
+        kernel_override("mx_cfg", cfg)
         ref = ops.q4_gemv(qw, sc, x, group, residual=res)
         assert torch.equal(ops.q4_gemv_t16(*tp, x, n, k, group, residual=res), ref)
         want = torch.empty(n, device=dev)
         LIB.call("q4_gemv_fused", ptr(qw), ptr(sc), ptr(x), ops.PRO_RMSNORM, ptr(nw), 1e-5, ptr(want), None, n, k,
                  group, stream_of(dev))
         assert torch.equal(ops.q4_gemv_t16(*tp, x, n, k, group, norm_w=nw), want)
-    monkeypatch.delenv("Q4_MX_CFG")
+    kernel_override("mx_cfg", None)
     # the automatic choice against the fp64 oracle (it may take a different entry from the reference layout)
     from oracle import llama_q4_ref as R
     oracle = (R.dequantize_q4(qw.cpu(), sc.cpu(), group).double() @ x.cpu().double()) + res.cpu().double()
@@ -123,13 +123,13 @@ def test_plain_and_norm_bit_identical_on_every_entry(dev, n, k, group, monkeypat
 
 
 @pytest.mark.parametrize("inter,k,group", [(8192, 3072, 128), (704, 256, 32), (344, 256, 32)])
-def test_swiglu_epilogue_bit_identical(dev, inter, k, group, monkeypatch):
+def test_swiglu_epilogue_bit_identical(dev, inter, k, group, kernel_override):
     qw, sc = weights(dev, 2 * inter, k, group, inter)
     tp = ops.t16_pack(qw, sc, group, ops.PAIR_SWIGLU)
     x = torch.randn(k, device=dev)
     nw = torch.rand(k, device=dev) + 0.5
     for cfg in mx_entries(k, group, True):
-        monkeypatch.setenv("Q4_MX_CFG", str(cfg))
+        kernel_override("mx_cfg", cfg)
         got = ops.q4_gemv_t16(*tp, x, 2 * inter, k, group, norm_w=nw, epilogue=ops.EPI_SWIGLU)
         assert torch.equal(got, ops.q4_gemv_swiglu(qw, sc, x, group, norm_w=nw)), cfg
 
