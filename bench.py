@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-e2e] [--skip-cpu] [--skip-gemm]
                     [--skip-attn] [--skip-native] [--sweep-gemv]
+    python bench.py --plain-launches attn|gemv|w4a16|gemm [...]   (untimed, for rocprofv3 --pmc passes)
 
 Headline (the JSON line's `value`): BASELINE config 2, the int4 decode GEMV y = W x at N=5120,
 K=3072 (fused qkv), group 128, fp16 x / fp16 y, fp32 accumulation, in achieved HBM GB/s. A step is
@@ -44,14 +45,16 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 2 ** 20
 
-# HBM bytes per 5120x3072 launch from rocprofv3 counter passes over this bench's GEMV leg
-# (profiles/q4_gemv_5120x3072_traffic_pmc.md): FETCH_SIZE 4025.0 KiB x 1.99497 (the factor that maps
-# FETCH_SIZE of a plain 8,126,464-byte streaming read to its size) + WRITE_SIZE 24.0 KiB x 1.0.
-# Counters cannot be read inside a timed run, so the figure is carried here with its source.
+# Profiled constants. Counters cannot be read inside a timed run, so these figures are carried here
+# with their source files; tests/test_host_checks_cpu.py fails when a constant and its file disagree.
+# HBM bytes per 5120x3072 launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each calibrated
+# with a plain streaming read / fill of known size).
 GEMV_TRAFFIC_BYTES_5120x3072 = 8_247_054
-# Average kernel duration of the 5120x3072 launch in the rocprofv3 kernel trace of this bench's GEMV
-# leg (profiles/q4_gemv_5120x3072_kernel_stats.md); reported beside the live HIP-event figure.
+GEMV_TRAFFIC_SOURCE = "profiles/q4_gemv_5120x3072_traffic_pmc.md"
+# Average duration of the 5120x3072 kernel in the rocprofv3 kernel trace (every dispatch isolated by
+# the profiler, so an upper bound on back-to-back launches).
 GEMV_ROCPROF_AVG_US = 3.746
+GEMV_ROCPROF_SOURCE = "profiles/q4_gemv_5120x3072_kernel_stats.md"
 
 
 def log(*a):
@@ -66,7 +69,7 @@ def gemv_bytes(N, K, group, x_bytes=2, y_bytes=2):
 STREAM_TIMING_MAX_STEPS = 256
 
 
-def timed_steps(fn_list, steps, warmup, reps=7):
+def timed_steps(fn_list, steps, warmup, reps=7, mode=None):
     """Time exactly `steps` launches, `reps` times; launch i is fn_list[i % n] (a rotation over n
     buffers). Returns the ms per launch of each repetition.
 
@@ -78,7 +81,8 @@ def timed_steps(fn_list, steps, warmup, reps=7):
         after queueing, the start event must still be pending, which proves no launch of the region
         waited for the host (else the repetition is re-queued with a longer wait);
       * larger `steps`, and any run under rocprofv3: the region is one replay of a HIP graph of the `steps` launches (its ~10 us
-        of graph-launch cost is then under 0.5% of the region)."""
+        of graph-launch cost is then under 0.5% of the region).
+    `mode` ("stream" or "graph") forces one of the two (a profiled run always replays graphs)."""
     import torch
     from q4llm._lib import LIB
     n = len(fn_list)
@@ -98,7 +102,7 @@ def timed_steps(fn_list, steps, warmup, reps=7):
 
     rot = capture(range(n))
     # under a profiler dispatches serialize and the region cannot be queued ahead: graph replays only
-    stream_mode = steps <= STREAM_TIMING_MAX_STEPS and not under_profiler()
+    stream_mode = (steps <= STREAM_TIMING_MAX_STEPS if mode is None else mode == "stream") and not under_profiler()
     ga = None if stream_mode else capture(range(steps))
     out = []
     with torch.cuda.stream(s):
@@ -233,11 +237,11 @@ def probe_read(dev, nbytes, loads):
     return ms * 1e3, nbytes / ms / 1e6
 
 
-def probe_empty(grid, block=256):
+def probe_empty(grid, block=256, steps=512, mode=None):
     import torch
     from q4llm._lib import LIB
     fns = [lambda: LIB.call("q4_probe_empty", grid, block, torch.cuda.current_stream().cuda_stream)] * 64
-    return stats_us(timed_steps(fns, 512, 64, 5))["median"]
+    return stats_us(timed_steps(fns, steps, 64, 5, mode))["median"]
 
 
 def cpu_gemv_baseline(N, K, group, seconds=10.0):
@@ -355,6 +359,67 @@ def bench_gemm(dev, shapes=GEMM_SHAPES, reps=5, vendor=False):
     return out
 
 
+# The reference's tuned results on its Adreno target (gemm/runs/run2/final_table.json:2-97): GFLOP/s of
+# the best schedule found ("tuned") and that device's attainable GFLOP/s ("roof") per problem, carried
+# here (the reference tree is not present where the bench runs) so each row prints beside them.
+REF_ADRENO_TUNED = {"S1": (173.1, 920.8), "S2": (107.2, 920.8), "S3": (127.4, 920.8), "S4": (69.5, 250.8),
+                    "S5": (93.5, 920.8), "S6": (98.6, 490.3), "S7": (15.4, 15.8), "S8": (161.2, 920.8)}
+
+
+def bench_ref_shapes(dev, reps=5):
+    """The reference's eight GEMM problems S1-S8 (gemm/shapes.py:41-66) with its own data recipe and
+    check (TOL 5e-3 of max|Cref| against the fp32 product of the fp16 inputs), timed on gemm_f16_nt_ws.
+    The kernel is NT: problems stored in another layout (NN, TN, TT) run on their logical A [M, K] and
+    B^T [N, K]; the one-time transposes that a caller holding such data would do are timed separately
+    (`layout_prep_us`, torch transpose copies). Operands stay resident (B rotated over up to 64 copies),
+    attainable = min(2.5 PFLOP/s, flops / compulsory bytes x 8 TB/s) as gemm/analyze.py:32-36."""
+    import numpy as np
+    import torch
+    from q4llm import ops, synth
+    out = {}
+    for sid, name, M, N, K, lay in synth.REF_GEMM_SHAPES:
+        a, b = synth.ref_gemm_problem(sid)
+        cref = a.astype(np.float32) @ b.astype(np.float32)
+        A = torch.from_numpy(a).to(dev)
+        Bt0 = torch.from_numpy(np.ascontiguousarray(b.T)).to(dev)
+        nb = min(64, max(2, -(-2 * MALL_BYTES // (2 * N * K))))
+        Bts = [Bt0.clone() for _ in range(nb)]
+        C = torch.empty(M, N, dtype=torch.float16, device=dev)
+        ws = torch.empty(max(ops.gemm_f16_nt_ws_bytes(M, N, K), 16), dtype=torch.uint8, device=dev)
+        ops.gemm_f16_nt_ws(A, Bt0, out=C, workspace=ws)
+        err = float(np.abs(C.cpu().float().numpy() - cref).max() / np.abs(cref).max())
+        fns = [lambda B=B: ops.gemm_f16_nt_ws(A, B, out=C, workspace=ws) for B in Bts]
+        st = stats_us(timed_steps(fns, max(64, 2 * len(fns)), len(fns), reps))
+        prep = None
+        if lay != "NT":
+            # the stored operands a caller would hold: A^T [K, M] for 'T' A, B [K, N] for 'N' B
+            As = torch.from_numpy(np.ascontiguousarray(a.T) if lay[0] == "T" else a).to(dev)
+            Bs = torch.from_numpy(b if lay[1] == "N" else np.ascontiguousarray(b.T)).to(dev)
+
+            def prep_fn():
+                if lay[0] == "T":
+                    As.t().contiguous()
+                if lay[1] == "N":
+                    Bs.t().contiguous()
+            prep = stats_us(timed_steps([prep_fn], 64, 8, reps))["median"]
+        flops = 2.0 * M * N * K
+        byts = 2.0 * (M * K + K * N + M * N)
+        gf = flops / st["median"] / 1e3
+        attain = min(MFMA_F16_PEAK_TFLOPS * 1e3, flops / byts * HBM_PEAK_GBS)
+        ref_tuned, ref_roof = REF_ADRENO_TUNED[sid]
+        out[sid] = {"name": name, "M": M, "N": N, "K": K, "layout": lay, "us": st["median"], "us_min": st["min"],
+                    "GFLOP/s": round(gf, 1), "attainable_GFLOP/s": round(attain, 1),
+                    "frac_attainable": round(gf / attain, 4), "err_over_max_ref": float(f"{err:.3e}"),
+                    "within_ref_tol": err <= synth.REF_GEMM_TOL, "layout_prep_us": prep,
+                    "ref_adreno_tuned_GFLOP/s": ref_tuned, "ref_adreno_frac_attainable": round(ref_tuned / ref_roof, 4)}
+        log(f"ref {sid} {name} {M}x{N}x{K} {lay}: {st['median']:.2f} us {gf:.0f} GFLOP/s "
+            f"({gf / attain:.1%} of attainable; Adreno tuned {ref_tuned} = {ref_tuned / ref_roof:.1%}); err {err:.1e}"
+            + (f"; layout prep {prep:.2f} us" if prep is not None else ""))
+        del A, Bt0, Bts, C, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 W4A16_SHAPES = [(256, 5120, 3072), (256, 3072, 3072), (256, 16384, 3072), (256, 3072, 8192)]
 
 
@@ -374,11 +439,13 @@ def bench_w4a16(dev, reps=5):
     g = torch.Generator().manual_seed(0)
     for (M, N, K) in W4A16_SHAPES:
         w = torch.randn(N, K, generator=g) * 0.02
-        qw, sc = R.quantize_q4(w, 128)
+        qd, sd = ops.quantize_q4(w.to(dev), 128)
+        qw, sc = R.quantize_q4(w, 128)  # the checker's copy: bit-identical to the GPU quantizer's
+        assert torch.equal(qd.cpu(), qw) and torch.equal(sd.cpu().view(torch.int16), sc.view(torch.int16))
         x = torch.randn(M, K, generator=g)
         wbytes = N * K // 2 + N * (K // 128) * 2
         nb = max(4, -(-2 * MALL_BYTES // wbytes))
-        copies = [(qw.to(dev), sc.to(dev)) for _ in range(nb)]
+        copies = [(qd.clone(), sd.clone()) for _ in range(nb)]
         xd = x.to(dev)
         y = torch.empty(M, N, device=dev)
         ws = torch.empty(ops.q4_linear_ws_split_bytes(M, N, K, 128), dtype=torch.uint8, device=dev)
@@ -395,11 +462,20 @@ def bench_w4a16(dev, reps=5):
         fns = [lambda q=q, s_=s_: ops.q4_linear_ws(xd, q, s_, 128, out=y, workspace=ws) for q, s_ in copies]
         st = stats_us(timed_steps(fns, max(16, 2 * len(fns)), len(fns), reps))
         flops = 2.0 * M * N * K
+        tf = flops / st["median"] / 1e6
+        byts = M * K * 4 + wbytes + M * N * 4
+        attain = min(MFMA_F16_PEAK_TFLOPS, flops / byts * HBM_PEAK_GBS / 1e3)
+        # issued: every k step runs two fp16 MFMAs (x split into hi + lo) for exact fp32 activations
         out[f"{M}x{N}x{K}"] = {"us": st["median"], "us_min": st["min"], "reps": st["reps"],
-                               "TFLOP/s": round(flops / st["median"] / 1e6, 1), "err_over_rms": float(f"{err:.3e}"),
+                               "TFLOP/s": round(tf, 1), "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                               "issued_mfma_TFLOP/s": round(2 * tf, 1),
+                               "frac_mfma_peak_issued": round(2 * tf / MFMA_F16_PEAK_TFLOPS, 4),
+                               "attainable_TFLOP/s": round(attain, 1), "frac_attainable": round(tf / attain, 4),
+                               "err_over_rms": float(f"{err:.3e}"),
                                "cpu_ms": round(cpu_ms, 3), "cpu_cores": cores, "cpu_reps": cpu_n}
-        log(f"w4a16 {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}); host QLinear {cpu_ms:.1f} ms; "
-            f"err/rms {err:.2e}")
+        log(f"w4a16 {M}x{N}x{K}: {st['median']:.2f} us (min {st['min']:.2f}) {tf:.0f} TFLOP/s useful "
+            f"({tf / MFMA_F16_PEAK_TFLOPS:.1%} of the fp16 peak, {2 * tf / MFMA_F16_PEAK_TFLOPS:.1%} issued); "
+            f"host QLinear {cpu_ms:.1f} ms; err/rms {err:.2e}")
         del copies, xd, y, ws
         torch.cuda.empty_cache()
     return out
@@ -450,6 +526,19 @@ def bench_attn(dev, reps=5):
 
 LAYER_BYTES_3B = 51_904_512     # wqkv + wo + wgu + wdown packed weights + fp16 scales, one layer
 LM_HEAD_BYTES_3B = 203_157_504  # tied int4 embedding as the LM head
+LAYER_PARAMS_3B = (5120 + 3072) * 3072 + 16384 * 3072 + 3072 * 8192  # weights per layer (qkv, o, gate/up, down)
+
+
+def prefill_roofline_3b(n_prompt, chunk, n_layers=28, n_q=24, hd=128):
+    """Useful flops per prompt token of the 3B prefill: 2 x the layer weights (the LM head runs on one row
+    per chunk) plus the attention's QK^T and PV over each row's valid keys (4 n_q hd per key and layer),
+    averaged over the prompt's causal rows; and the roofline rate min(fp16 MFMA peak / flops, HBM / bytes),
+    bytes = one read of every layer weight per chunk spread over its rows."""
+    avg_valid = (n_prompt + 1) / 2
+    flops = 2.0 * n_layers * LAYER_PARAMS_3B + 4.0 * n_layers * n_q * hd * avg_valid
+    bytes_per_tok = n_layers * LAYER_BYTES_3B / chunk
+    rate = min(MFMA_F16_PEAK_TFLOPS * 1e12 / flops, HBM_PEAK_GBS * 1e9 / bytes_per_tok)
+    return flops, rate
 
 
 def cpu_decode_baseline(pc, host_tensors, token, pos=700, L=1024, max_steps=3, budget_s=20.0):
@@ -520,6 +609,7 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
     kv_valid = n_layers * 2 * avg_valid * 8 * 128 * 2
     kv_bucket = n_layers * 2 * 1024 * 8 * 128 * 2
     tok_s = res["decode_tok_s"]
+    pf_flops, pf_roof = prefill_roofline_3b(len(prompt), 256)
     out = {
         "decode_tok_s": tok_s, "prefill_tok_s": res["prefill_tok_s"], "ttft_ms": res["ttft_ms"],
         "decode_steps": res["decode_steps"], "gpu_ms_per_decode_step": round(gpu_ms, 4),
@@ -528,6 +618,8 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
         "hbm_roofline_tok_s_L1024": round(HBM_PEAK_GBS * 1e9 / (w_bytes + kv_bucket), 1),
         "frac_hbm_roofline": round(tok_s * (w_bytes + kv_valid) / (HBM_PEAK_GBS * 1e9), 4),
         "frac_hbm_roofline_gpu_only": round((w_bytes + kv_valid) / (gpu_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "prefill_flops_per_token": round(pf_flops), "prefill_roofline_tok_s": round(pf_roof, 1),
+        "frac_prefill_roofline": round(res["prefill_tok_s"] / pf_roof, 4),
         "tokens_sha1": hashlib.sha1(json.dumps(res["tokens"]).encode()).hexdigest(),
         "first_tokens": res["tokens"][:16], "model_build_s": round(build_s, 1),
         "buckets_used": sorted({L for L, _ in res["steps"]}),
@@ -569,6 +661,88 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
     return out, res["tokens"]
 
 
+# ------------------------------------------------------------------------------------------------
+# plain launches for hardware-counter passes
+# ------------------------------------------------------------------------------------------------
+
+
+def plain_launches(dev, what, Ls, shapes, iters, probe_bytes, vendor):
+    """Plain stream launches of one leg's calls, a device synchronisation after each, then a streaming-
+    read probe of a known byte count whose counter reading calibrates the pass. rocprofv3's counter
+    mode (--pmc) samples every dispatch; this gives it a short, graph-free sequence of the launches the
+    timed legs replay from graphs, each reading its operands from memory (rotating copies). One line
+    per leg names the algorithmic bytes (or flops) per launch that the counters are compared with."""
+    import math
+    import torch
+    from q4llm import ops, synth
+    from q4llm._lib import LIB
+    sync = torch.cuda.synchronize
+    if what == "attn":
+        for L in Ls:
+            q, k, v, valid = synth.attn_problem(L, seed=0)
+            qd = torch.from_numpy(q).to(dev)
+            ks = [torch.from_numpy(k).to(dev) for _ in range(8)]
+            vs = [torch.from_numpy(v).to(dev) for _ in range(8)]
+            start = torch.tensor([valid - 1], dtype=torch.int32, device=dev)
+            ws = torch.empty(ops.attn_workspace_bytes(1, 24, 8, 128, L), dtype=torch.uint8, device=dev)
+            o = torch.empty(1, 24 * 128, dtype=torch.float32, device=dev)
+            for i in range(iters):
+                ops.attn_bucket(qd, ks[i % 8], vs[i % 8], L, start, 1 / math.sqrt(128), ws, o)
+                sync()
+            print(f"attn L={L} valid={valid} launches={iters}: K/V bytes of the valid rows {2 * valid * 8 * 128 * 2}, "
+                  f"q + out {24 * 128 * 4 * 2}", flush=True)
+            del ks, vs
+    elif what == "gemv":
+        N, K, group = 5120, 3072, 128
+        qw, sc, x = synth.gemv_problem(N, K, group)
+        qws = [torch.from_numpy(qw).to(dev) for _ in range(8)]
+        scs = [torch.from_numpy(sc).to(dev) for _ in range(8)]
+        xd = torch.from_numpy(x).to(dev)
+        y = torch.empty(N, dtype=torch.float16, device=dev)
+        for i in range(iters):
+            ops.q4_gemv(qws[i % 8], scs[i % 8], xd, group, out=y)
+            sync()
+        print(f"gemv {N}x{K} launches={iters}: algorithmic bytes {gemv_bytes(N, K, group)}", flush=True)
+    elif what == "w4a16":
+        g = torch.Generator().manual_seed(0)
+        for (M, N, K) in shapes or W4A16_SHAPES:
+            qw, sc = ops.quantize_q4((torch.randn(N, K, generator=g) * 0.02).to(dev), 128)
+            copies = [(qw.clone(), sc.clone()) for _ in range(8)]
+            xd = torch.randn(M, K, generator=g).to(dev)
+            y = torch.empty(M, N, device=dev)
+            ws = torch.empty(ops.q4_linear_ws_split_bytes(M, N, K, 128), dtype=torch.uint8, device=dev)
+            for i in range(iters):
+                ops.q4_linear_ws(xd, copies[i % 8][0], copies[i % 8][1], 128, out=y, workspace=ws)
+                sync()
+            print(f"w4a16 {M}x{N}x{K} launches={iters}: useful flops {2 * M * N * K}", flush=True)
+            del copies
+    elif what == "gemm":
+        for (M, N, K) in shapes or [(4096, 4096, 4096)]:
+            a, b = synth.gemm_problem(M, N, K, seed=0)
+            A = torch.from_numpy(a).to(dev)
+            Bs = [torch.from_numpy(b).to(dev) for _ in range(2)]
+            C = torch.empty(M, N, dtype=torch.float16, device=dev)
+            ws = torch.empty(max(ops.gemm_f16_nt_ws_bytes(M, N, K), 16), dtype=torch.uint8, device=dev)
+            for i in range(iters):
+                ops.gemm_f16_nt_ws(A, Bs[i % 2], out=C, workspace=ws)
+                sync()
+            if vendor:
+                for i in range(iters):
+                    torch.matmul(A, Bs[i % 2].t())
+                    sync()
+            print(f"gemm {M}x{N}x{K} launches={iters}{' (+ torch.matmul)' if vendor else ''}: flops {2 * M * N * K}",
+                  flush=True)
+            del A, Bs, C, ws
+    if probe_bytes:
+        buf = torch.ones(probe_bytes // 4, dtype=torch.int32, device=dev)
+        sink = torch.empty(1, dtype=torch.float32, device=dev)
+        for _ in range(iters):
+            LIB.call("q4_probe_read", buf.data_ptr(), probe_bytes, sink.data_ptr(), 1,
+                     torch.cuda.current_stream().cuda_stream)
+            sync()
+        print(f"probe read_kernel<1> launches={iters}: bytes read {probe_bytes}", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -590,6 +764,15 @@ def main():
     ap.add_argument("--gemm-shapes", nargs="*", default=None, metavar="MxNxK",
                     help="run the GEMM leg on these shapes only (default: every config-3 shape)")
     ap.add_argument("--tokens-out", default=None, help="write the e2e generated token ids here")
+    ap.add_argument("--plain-launches", choices=["attn", "gemv", "w4a16", "gemm"], default=None,
+                    help="no timing: plain launches of one leg, a sync after each, for rocprofv3 --pmc passes")
+    ap.add_argument("--plain-L", type=int, nargs="*", default=[1024, 4096], help="--plain-launches attn buckets")
+    ap.add_argument("--plain-shapes", nargs="*", default=None, metavar="MxNxK",
+                    help="--plain-launches w4a16 / gemm shapes (default: the W4A16 leg's shapes / 4096^3)")
+    ap.add_argument("--plain-iters", type=int, default=40)
+    ap.add_argument("--plain-vendor", action="store_true", help="--plain-launches gemm: also torch.matmul")
+    ap.add_argument("--plain-probe", type=int, default=8126464,
+                    help="bytes of the calibration read probe after the plain launches (0: none)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported: this build runs on a single "
@@ -606,6 +789,11 @@ def main():
     dev = torch.device("cuda:0")
     from q4llm._lib import LIB
     LIB.load()
+    if a.plain_launches:
+        plain_launches(dev, a.plain_launches, a.plain_L,
+                       None if a.plain_shapes is None else [tuple(int(v) for v in t.split("x")) for t in a.plain_shapes],
+                       a.plain_iters, a.plain_probe, a.plain_vendor)
+        return 0
 
     shapes = [(5120, 3072), (16384, 3072), (3072, 8192)]
     results = {}
@@ -616,6 +804,8 @@ def main():
             out["gemm_f16"] = bench_gemm(dev, GEMM_SHAPES if a.gemm_shapes is None else
                                          [tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes],
                                          vendor=a.vendor_gemm)
+            if a.gemm_shapes is None:
+                out["gemm_ref_shapes"] = bench_ref_shapes(dev)
         if not a.skip_attn:
             out["attn_decode"] = bench_attn(dev)
         if not a.skip_w4a16:
@@ -636,6 +826,13 @@ def main():
         us = st["median"]
         results[(N, K)] = dict(us=us, us_min=st["min"], us_max=st["max"], reps=st["reps"], gbs=gb.bytes / us / 1e3,
                                bytes=gb.bytes, err=rel, steps=steps, copies=len(gb.qws))
+        if (N, K) == shapes[0]:
+            # both launch modes beside the value, over long regions: plain stream launches (the mode
+            # --steps <= 256 selects; 256 launches, the most the region queues ahead) and graph replays
+            # (the mode the model's step runs in; 2048 launches)
+            results[(N, K)]["modes"] = {
+                "stream_256": stats_us(timed_steps(gb.launches(), STREAM_TIMING_MAX_STEPS, a.warmup, 5, "stream"))["median"],
+                "graph_2048": stats_us(timed_steps(gb.launches(), 2048, a.warmup, 5, "graph"))["median"]}
         log(f"gemv N={N} K={K}: {us:.3f} us/launch (min {st['min']:.3f}, max {st['max']:.3f} over {st['reps']} reps "
             f"of {steps}), {gb.bytes / us / 1e3:.1f} GB/s, err/rms {rel:.2e}")
         del gb
@@ -647,7 +844,9 @@ def main():
         probes[f"read_{nbytes}B"] = {"us": round(us, 3), "GB/s": round(gbs, 1)}
         log(f"probe read {nbytes} B: {us:.3f} us {gbs:.1f} GB/s")
     probes["empty_kernel_us"] = round(probe_empty(256), 3)
-    log(f"probe empty kernel: {probes['empty_kernel_us']} us per launch")
+    probes["empty_kernel_stream_us"] = round(probe_empty(256, steps=256, mode="stream"), 3)
+    log(f"probe empty kernel: {probes['empty_kernel_us']} us per launch in graph replays, "
+        f"{probes['empty_kernel_stream_us']} us as plain stream launches")
     torch.cuda.empty_cache()
 
     head = results[shapes[0]]
@@ -668,16 +867,26 @@ def main():
         "config": {"workload": "int4 decode GEMV y=Wx, N=5120 (fused qkv), K=3072, group 128, batch 1",
                    "N": 5120, "K": 3072, "group": 128, "weight_copies_rotated": head["copies"]},
         "timing": {"statistic": "median over repetitions of the timed region (value, ms_per_step)",
-                   "reps": head["reps"], "steps_per_rep": head["steps"], "us_per_step_median": head["us"],
-                   "us_per_step_min": head["us_min"], "us_per_step_max": head["us_max"]},
+                   "reps": head["reps"], "steps_per_rep": head["steps"],
+                   "launch_mode": "stream" if head["steps"] <= STREAM_TIMING_MAX_STEPS else "graph",
+                   "us_per_step_median": head["us"],
+                   "us_per_step_min": head["us_min"], "us_per_step_max": head["us_max"],
+                   "us_per_launch_by_mode": head["modes"],
+                   "note": "value is the launch mode this command's --steps selects (plain stream launches up to "
+                           f"{STREAM_TIMING_MAX_STEPS} steps, one graph replay above); both modes over long regions "
+                           "are reported beside it"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
                      "frac_at_min": round(head["bytes"] / head["us_min"] / 1e3 / HBM_PEAK_GBS, 4),
                      "traffic": GEMV_TRAFFIC_BYTES_5120x3072,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+                     "traffic_source": f"profiled constant, {GEMV_TRAFFIC_SOURCE}",
                      "algorithmic_bytes_per_launch": head["bytes"], "avg_launch_us": round(head["us"], 4),
-                     "rocprof_avg_kernel_us": GEMV_ROCPROF_AVG_US,
-                     "frac_at_rocprof_avg": round(head["bytes"] / GEMV_ROCPROF_AVG_US / 1e3 / HBM_PEAK_GBS, 4),
+                     "rocprof_profile": {"avg_kernel_us": GEMV_ROCPROF_AVG_US, "source": GEMV_ROCPROF_SOURCE,
+                                         "frac_at_avg": round(head["bytes"] / GEMV_ROCPROF_AVG_US / 1e3 /
+                                                              HBM_PEAK_GBS, 4),
+                                         "note": "profiled constant: rocprofv3 kernel-trace average of "
+                                                 "isolated dispatches, not this run"},
                      "measured_read_floor_us_same_bytes": floor,
                      "frac_of_measured_read_floor": round(floor / head["us"], 4)},
         "gemv_shapes": {f"{N}x{K}": {"us": round(r["us"], 3), "us_min": round(r["us_min"], 3),
@@ -689,6 +898,8 @@ def main():
         shapes = ([tuple(int(v) for v in t.split("x")) for t in a.gemm_shapes] if a.gemm_shapes is not None
                   else GEMM_SHAPES)
         out["gemm_f16"] = bench_gemm(dev, shapes, vendor=a.vendor_gemm)
+        if a.gemm_shapes is None:
+            out["gemm_ref_shapes"] = bench_ref_shapes(dev)
     if not a.skip_attn:
         out["attn_decode"] = bench_attn(dev)
     if not a.skip_w4a16:

@@ -148,6 +148,27 @@ def gemm_problem(M, N, K, seed=0):
     return a, b
 
 
+# The reference's eight GEMM problems (gemm/shapes.py:41-50): id, name, M, N, K, stored layout of A
+# and B in BLAS letters (N as written, T stored transposed; B "T" is a PyTorch Linear weight [N, K]).
+REF_GEMM_SHAPES = [
+    ("S1", "square_nn", 1024, 1024, 1024, "NN"), ("S2", "prefill_nt", 128, 3072, 3072, "NT"),
+    ("S3", "skinny_tn", 4096, 64, 1024, "TN"), ("S4", "flat_nt", 16, 4096, 4096, "NT"),
+    ("S5", "largek_tt", 256, 256, 8192, "TT"), ("S6", "smallk_nn", 2048, 2048, 32, "NN"),
+    ("S7", "gemv_nt", 1, 4096, 4096, "NT"), ("S8", "regular_tn", 768, 768, 768, "TN"),
+]
+REF_GEMM_TOL = 5e-3  # max|C - Cref| / max|Cref| (gemm/shapes.py:53)
+
+
+def ref_gemm_problem(sid, seed=0):
+    """The reference's data for problem `sid` (gemm/shapes.py:56-62): logical A [M, K] and B [K, N],
+    fp16 U(-1, 1) from default_rng(seed + problem number), A drawn first."""
+    _, _, M, N, K, _ = next(t for t in REF_GEMM_SHAPES if t[0] == sid)
+    rng = np.random.default_rng(seed + int(sid[1:]))
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float16)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float16)
+    return a, b
+
+
 def attn_problem(L, n_q=24, n_kv=8, hd=128, seed=0):
     """q [1, n_q, hd], K/V caches [L, n_kv, hd] fp16 N(0, 1), valid length
     uniform in [1, L] (the query sits at position valid - 1)."""

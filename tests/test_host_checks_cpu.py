@@ -104,3 +104,22 @@ def test_lazy_safetensors_reads_two_shards(tmp_path, dtype):
         t = lazy[k]
         assert t.dtype == dtype and torch.equal(t, sd[k].to(dtype))
     assert "model.layers.99.mlp.up_proj.weight" not in lazy
+
+
+def test_bench_profiled_constants_match_their_profiles():
+    """bench.py carries two figures it cannot measure inside a timed run (the GEMV's counter-measured
+    traffic and its rocprofv3 average); each must equal the figure in the profile file it names."""
+    import pathlib
+    import re
+    import sys
+    root = pathlib.Path(__file__).resolve().parent.parent
+    sys.path.insert(0, str(root))
+    import bench
+    traffic = (root / bench.GEMV_TRAFFIC_SOURCE).read_text()
+    assert f"{bench.GEMV_TRAFFIC_BYTES_5120x3072:,}" in traffic
+    stats = (root / bench.GEMV_ROCPROF_SOURCE).read_text()
+    row = next(line for line in stats.splitlines() if "N=5120, K=3072" in line and line.startswith("|"))
+    avg = float(row.split("|")[3])
+    assert avg == bench.GEMV_ROCPROF_AVG_US, (row, bench.GEMV_ROCPROF_AVG_US)
+    for text in (stats, traffic):  # each names the committed command that produced it
+        assert re.search(r"rocprofv3 .*bench\.py", text, re.S)
