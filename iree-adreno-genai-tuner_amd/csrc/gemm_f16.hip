@@ -491,9 +491,17 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // pipelined ones replace them), the pipelined schedule on the 8-wave 256x256 and the two-workgroup
 // 128x128 entries, and a ping-pong schedule of two 4-wave groups on 256x256: each equal or slower on
 // every config-3 shape.
-int choose_tile(int64_t M, int64_t N, bool split_ok) {
+// Problems under 4 GFLOP (under ~2 us of matrix-core time at the dense peak) are set by latency and
+// by how many CUs stream at once, not by the tile's operand reuse.
+bool small_problem(int64_t M, int64_t N, int64_t K) { return 2.0 * M * N * K < 4e9; }
+
+int choose_tile(int64_t M, int64_t N, int64_t K, bool split_ok) {
   const int ov = debug_override(Q4_DBG_GEMM_TILE);
   if (ov >= 0 && ov < kNumTiles) return ov;
+  (void)split_ok;
+  // small problems (the reference's S1-S6 and S8): 64x64, the K split below (swept on every entry and
+  // splits of 1-32: S1 1024^3 15.3 -> 9.0 us, S3 15.3 -> 8.3, S5 19.5 -> 12.0, S8 12.7 -> 7.2)
+  if (small_problem(M, N, K)) return 5;
   auto tiles = [&](int i) { return cdiv(M, kTiles[i].bm) * cdiv(N, kTiles[i].bn); };
   if (M >= 512) return tiles(0) >= 256 ? 0 : (tiles(6) >= 240 && tiles(6) <= 256 ? 6 : 1);
   if (split_ok && N % 4 == 0) return 2;
@@ -522,6 +530,8 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, int ti) {
   const int nk = static_cast<int>(cdiv(K, t.bk));
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   int want = M < 512 ? static_cast<int>(std::min<int64_t>(256 / tiles, nk / 4)) : 1;
+  // small problems: about 256 workgroups (256 / tiles rounded), each K range at least 8 K steps
+  if (small_problem(M, N, K)) want = static_cast<int>(std::min<int64_t>((512 / tiles + 1) / 2, nk / 8));
   if (debug_set(Q4_DBG_GEMM_SPLIT)) want = debug_override(Q4_DBG_GEMM_SPLIT);
   if (want <= 1 || nk < 2) return p;
   const int nk_s = static_cast<int>(cdiv(nk, std::min(want, nk)));
@@ -551,7 +561,7 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
       hipLaunchKernelGGL((gemv_f16_kernel<2, 8>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
     return launch_status();
   }
-  const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N, part != nullptr);
+  const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N, K, part != nullptr);
   const TileCfg& t = kTiles[ti];
   const int tiles_m = static_cast<int>(cdiv(M, t.bm)), tiles_n = static_cast<int>(cdiv(N, t.bn));
   const int ntiles = tiles_m * tiles_n;
@@ -587,7 +597,7 @@ int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M
 // Workspace bytes gemm_f16_nt_ws uses for this shape (0: no K split).
 size_t gemm_f16_ws_bytes(int64_t M, int64_t N, int64_t K) {
   if (M == 1) return 0;
-  return gemm_split_bytes(M, N, K, choose_tile(M, N, true));
+  return gemm_split_bytes(M, N, K, choose_tile(M, N, K, true));
 }
 
 int gemm_f16_num_tiles() { return kNumTiles; }

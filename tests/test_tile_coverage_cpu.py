@@ -258,6 +258,8 @@ def gemm_split(cfg, M, N, K, force=None):
     nk = cdiv(K, bk)
     tiles = cdiv(M, bm) * cdiv(N, bn)
     want = min(256 // tiles, nk // 4) if M < 512 else 1
+    if 2.0 * M * N * K < 4e9:  # small problems: ~256 workgroups, K ranges of >= 8 steps
+        want = min((512 // tiles + 1) // 2, nk // 8)
     if force is not None:
         want = force
     if want <= 1 or nk < 2:
@@ -375,6 +377,14 @@ def test_gemm_split_rule_fills_the_cus():
     assert gemm_split(cfg, 256, 3072, 8192) == (5, 26)   # 48 tiles x 5 (last range 24 steps)
     assert gemm_split(cfg, 256, 16384, 3072) == (1, 0)   # 256 tiles fill the CUs
     assert gemm_split(cfg, 1024, 5120, 3072) == (1, 0)   # no split from 512 rows on
+    # problems under 4 GFLOP (the reference's S1-S8) take the 64x64 entry and about 256 workgroups
+    c64 = next(c for c in config_table("gemm") if c[:2] == (64, 64))
+    assert gemm_split(c64, 1024, 1024, 1024) == (1, 0)   # S1: 256 tiles
+    assert gemm_split(c64, 128, 3072, 3072) == (3, 16)   # S2: 96 tiles x 3
+    assert gemm_split(c64, 4096, 64, 1024) == (2, 8)     # S3: 64 tiles x 2 (8-step ranges)
+    assert gemm_split(c64, 16, 4096, 4096) == (4, 16)    # S4: 64 tiles x 4
+    assert gemm_split(c64, 256, 256, 8192) == (16, 8)    # S5: 16 tiles x 16
+    assert gemm_split(c64, 768, 768, 768) == (1, 0)      # S8: 144 tiles, 12 steps
 
 
 # ------------------------------------------------------------------------------------------------
@@ -608,3 +618,4 @@ def test_linear_ws_t16_loads_and_outputs(pairing, N, K, group):
                 assert col == t16_row(vc, N, pairing, hd)
                 seen[col] += 1
         assert (seen == 1).all()
+
