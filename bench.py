@@ -49,11 +49,11 @@ MALL_BYTES = 256 * 2 ** 20
 # with their source files; tests/test_host_checks_cpu.py fails when a constant and its file disagree.
 # HBM bytes per 5120x3072 launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each calibrated
 # with a plain streaming read / fill of known size).
-GEMV_TRAFFIC_BYTES_5120x3072 = 8_247_054
+GEMV_TRAFFIC_BYTES_5120x3072 = 8_234_776
 GEMV_TRAFFIC_SOURCE = "profiles/q4_gemv_5120x3072_traffic_pmc.md"
 # Average duration of the 5120x3072 kernel in the rocprofv3 kernel trace (every dispatch isolated by
 # the profiler, so an upper bound on back-to-back launches).
-GEMV_ROCPROF_AVG_US = 3.746
+GEMV_ROCPROF_AVG_US = 3.670
 GEMV_ROCPROF_SOURCE = "profiles/q4_gemv_5120x3072_kernel_stats.md"
 
 

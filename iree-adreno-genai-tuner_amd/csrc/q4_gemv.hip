@@ -661,9 +661,12 @@ int choose_cfg(int64_t N, int64_t K, bool paired) {
     if (K == 3072 && N == 16384) return 6;
   } else {
     if (K == 3072) {
-      // 10 rows per workgroup: 512 workgroups, two per CU, so every CU streams the same bytes (the
-      // 12-row entry leaves 171 CUs with two workgroups and 85 with one; 3.45 -> 3.39 us)
-      if (N == 5120) return 1;
+      // 5120 rows: 20 rows per workgroup with 16 lanes per row, 256 workgroups, one per CU, equal
+      // bytes everywhere. Against the 10-row entry (512 workgroups, two per CU), three alternating
+      // rounds on one MI355X: plain stream launches 3.74-3.76 us against 3.83-3.89 (20 launches),
+      // 3.65 against 3.78 (256); graph replays 3.43 against 3.42. Stream launches are how a caller of
+      // the C ABI issues single GEMVs, and the model's fp32-x projections take the matrix-core kernel.
+      if (N == 5120) return 4;
       if (N == 16384) return 7;
       if (N == 3072) return 8;
       if (N > 65536) return 19;
