@@ -397,41 +397,53 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
 // 16-byte chunks (8 k), kKc chunks per lane per pass, so one pass spans 512 * kKc k. Every load of a
 // pass (x and the rows) is issued before any use; v_dot2_f32_f16 with fp32 accumulation, then a
 // reduction over the wave. Rows past N and k past K read out of range (zeros). Memory bound.
-template <int kRows, int kKc>
-__global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ B,
-                                                       uint16_t* __restrict__ c, int N, int K, int ldb) {
+// fp16 GEMV (M == 1): C[0, n] = sum_k A[0, k] B[n, k]. kSplit waves share each row, wave q taking the
+// q-th contiguous part of every K pass; lane l of a wave reads 16 consecutive bytes of a row per load,
+// so one load instruction covers 1 KB of it. All loads of a pass are issued before use; the wave sums
+// are combined through LDS in wave order.
+template <int kKc, int kWaves, int kSplit>
+__global__ __launch_bounds__(64 * kWaves) void gemv_f16_kernel(const uint16_t* __restrict__ a,
+                                                               const uint16_t* __restrict__ B,
+                                                               uint16_t* __restrict__ c, int N, int K, int ldb) {
   typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  static_assert(kWaves % kSplit == 0, "whole rows per workgroup");
+  __shared__ float red[kWaves];
   const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kRows;
+  const int wave = threadIdx.x >> 6;
+  const int part = wave % kSplit;
+  const int row = blockIdx.x * (kWaves / kSplit) + wave / kSplit;
   const __amdgpu_buffer_rsrc_t br = make_rsrc(B, static_cast<uint32_t>(N - 1) * ldb * 2u + K * 2u);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a, K * 2u);
-  float acc[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) acc[r] = 0.0f;
-  for (int kb = 0; kb < K; kb += 512 * kKc) {
-    uint4 xv[kKc], wv[kRows][kKc];
+  float acc = 0.0f;
+  constexpr int kPass = 512 * kKc * kSplit;  // k per pass over all parts
+  for (int kb = 0; kb < K; kb += kPass) {
+    uint4 xv[kKc], wv[kKc];
 #pragma unroll
     for (int i = 0; i < kKc; ++i) {
-      const int k = kb + (i * 64 + lane) * 8;
+      const int k = kb + ((part * kKc + i) * 64 + lane) * 8;
       xv[i] = buf_load16(xr, k < K ? k * 2u : kOOB);
-#pragma unroll
-      for (int r = 0; r < kRows; ++r)
-        wv[r][i] = buf_load16(br, k < K && row0 + r < N ? (static_cast<uint32_t>(row0 + r) * ldb + k) * 2u : kOOB);
+      wv[i] = buf_load16(br, k < K && row < N ? (static_cast<uint32_t>(row) * ldb + k) * 2u : kOOB);
     }
 #pragma unroll
-    for (int i = 0; i < kKc; ++i)
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) {
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].x), __builtin_bit_cast(half2v, xv[i].x), acc[r], false);
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].y), __builtin_bit_cast(half2v, xv[i].y), acc[r], false);
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].z), __builtin_bit_cast(half2v, xv[i].z), acc[r], false);
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[r][i].w), __builtin_bit_cast(half2v, xv[i].w), acc[r], false);
-      }
+    for (int i = 0; i < kKc; ++i) {
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[i].x), __builtin_bit_cast(half2v, xv[i].x), acc, false);
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[i].y), __builtin_bit_cast(half2v, xv[i].y), acc, false);
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[i].z), __builtin_bit_cast(half2v, xv[i].z), acc, false);
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wv[i].w), __builtin_bit_cast(half2v, xv[i].w), acc, false);
+    }
   }
+  const float v = group_sum<64>(acc);
+  if constexpr (kSplit == 1) {
+    if (lane == 0 && row < N) c[row] = float_to_half_bits(v);
+  } else {
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    if (part == 0 && lane == 0 && row < N) {
+      float t = red[wave];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const float v = group_sum<64>(acc[r]);
-    if (lane == 0 && row0 + r < N) c[row0 + r] = float_to_half_bits(v);
+      for (int q = 1; q < kSplit; ++q) t += red[wave + q];
+      c[row] = float_to_half_bits(t);
+    }
   }
 }
 
@@ -549,16 +561,28 @@ size_t gemm_split_bytes(int64_t M, int64_t N, int64_t K, int ti) {
 
 int gemm_f16_launch(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                     int64_t ldb, int64_t ldc, int cfg, hipStream_t st, float* part = nullptr, size_t part_bytes = 0) {
-  if (M == 1 && cfg < 0) {  // 2 rows per wave, 8 per workgroup; passes of up to 4096 k
-    const unsigned grid = static_cast<unsigned>(cdiv(N, 8));
-    if (K <= 1024)
-      hipLaunchKernelGGL((gemv_f16_kernel<2, 2>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
-    else if (K <= 2048)
-      hipLaunchKernelGGL((gemv_f16_kernel<2, 4>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
-    else if (K <= 3072)
-      hipLaunchKernelGGL((gemv_f16_kernel<2, 6>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
-    else
-      hipLaunchKernelGGL((gemv_f16_kernel<2, 8>), dim3(grid), dim3(256), 0, st, A, B, C, (int)N, (int)K, (int)ldb);
+  if (M == 1 && cfg < 0) {
+    // One row per wave, 4 waves per workgroup; rows longer than 3072 are split over two waves (passes
+    // of up to 4096 k per row). Measured on one MI355X, graph replays over rotating B copies, against
+    // two rows per wave in 4-wave workgroups: 1x3072x3072 5.79 -> 5.22 us, 1x4096x4096 8.96 -> 7.79 us
+    // (7.93 without the split), 1x5120x3072 8.03 -> 7.36 us. Two rows per wave in 6- or 8-wave
+    // workgroups and one row per wave in 6- or 8-wave workgroups measured between the two.
+    constexpr int kWaves = 4;
+    const int split = K > 3072 ? 2 : 1;
+    const unsigned grid = static_cast<unsigned>(cdiv(N, kWaves / split));
+    auto go = [&](auto kc) {
+      constexpr int KC = decltype(kc)::value;
+      if (split == 2)
+        hipLaunchKernelGGL((gemv_f16_kernel<KC / 2, kWaves, 2>), dim3(grid), dim3(64 * kWaves), 0, st, A, B, C, (int)N,
+                           (int)K, (int)ldb);
+      else
+        hipLaunchKernelGGL((gemv_f16_kernel<KC, kWaves, 1>), dim3(grid), dim3(64 * kWaves), 0, st, A, B, C, (int)N,
+                           (int)K, (int)ldb);
+    };
+    if (K <= 1024) go(std::integral_constant<int, 2>{});
+    else if (K <= 2048) go(std::integral_constant<int, 4>{});
+    else if (K <= 3072) go(std::integral_constant<int, 6>{});
+    else go(std::integral_constant<int, 8>{});
     return launch_status();
   }
   const int ti = cfg >= 0 && cfg < kNumTiles ? cfg : choose_tile(M, N, K, part != nullptr);

@@ -157,6 +157,20 @@ def test_gemm_reference_nt_shapes_tol(dev, sid):
     assert np.abs(c - cref).max() / np.abs(cref).max() <= synth.REF_GEMM_TOL
 
 
+@pytest.mark.parametrize("N,K", [(300, 520), (7, 64), (1000, 8200), (33, 4096), (4096, 3080), (65, 12288)])
+def test_gemm_m1_gemv_ragged(dev, N, K):
+    """M == 1 takes the fp16 GEMV: one row per wave, rows longer than 3072 split over two waves; ragged N
+    (a partial last workgroup), K with a partial last pass, several passes (K > 4096), against the host
+    fp32 product of the same fp16 inputs."""
+    a, b = synth.gemm_problem(1, N, K, seed=3)
+    A, B = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    c = nan_like((1, N), torch.float16, dev)
+    ops.gemm_f16_nt(A, B, out=c)
+    ref = torch.from_numpy(a).float() @ torch.from_numpy(b).float().T
+    err = (c.cpu().float() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.pow(2).mean().sqrt().item(), (N, K, err)
+
+
 def test_gemm_all_tiles_and_ragged_edges(dev):
     from q4llm._lib import LIB
     n_cfg = LIB.raw("gemm_f16_num_configs")()
