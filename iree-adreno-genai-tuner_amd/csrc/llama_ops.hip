@@ -37,8 +37,9 @@ __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off
 // linear_reduce_kernel, so the same bits), and the completed row is written back to x. The first PB
 // partials load with the row, the rest one round trip each (PB 12 for more than 6 partials: the 128-row
 // prefill chunks have 8 and 10; 6 otherwise, where the 12-wide form measured 1.3% slower prefill).
-template <int PB = 6>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
+// TH threads per workgroup (256 or 1024), each holding 1024 / TH float4s of the row.
+template <int PB = 6, int TH = 256>
+__global__ __launch_bounds__(TH) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
                                                       const int32_t* __restrict__ row_sel,
                                                       uint16_t* __restrict__ xh, uint16_t* __restrict__ xl,
@@ -47,8 +48,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
   const int64_t row = row_sel ? min(max(static_cast<int64_t>(row_sel[0]), int64_t{0}), M - 1) : blockIdx.x;
   const float* xr = x + row * D;
   float* orow = out + static_cast<int64_t>(blockIdx.x) * D;
-  constexpr int kV = 4;
-  const bool vec = D % 4 == 0 && D <= 4 * 256 * kV;
+  static_assert(TH == 256 || TH == 1024, "threads per row");
+  constexpr int kV = 1024 / TH;
+  constexpr int kW = TH / 64;  // waves
+  const bool vec = D % 4 == 0 && D <= 4 * TH * kV;
   float4 v[kV], wv[kV];
   float s = 0.0f;
   if (vec) {
@@ -57,9 +60,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
     const __amdgpu_buffer_rsrc_t xres = row_rsrc(xr, static_cast<uint32_t>(D) * 4u);
     const __amdgpu_buffer_rsrc_t wres = row_rsrc(w, static_cast<uint32_t>(D) * 4u);
 #pragma unroll
-    for (int i = 0; i < kV; ++i) v[i] = load_f4(xres, (threadIdx.x + i * 256) * 16u);
+    for (int i = 0; i < kV; ++i) v[i] = load_f4(xres, (threadIdx.x + i * TH) * 16u);
 #pragma unroll
-    for (int i = 0; i < kV; ++i) wv[i] = load_f4(wres, (threadIdx.x + i * 256) * 16u);
+    for (int i = 0; i < kV; ++i) wv[i] = load_f4(wres, (threadIdx.x + i * TH) * 16u);
     if (n_split > 0) {
       // partial sp of this row: psum[sp][row][:]; the first kPb splits load with the row, the sums run
       // in ascending split order, as in linear_reduce_kernel
@@ -73,12 +76,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
       for (int sp = 0; sp < kPb; ++sp)
 #pragma unroll
         for (int i = 0; i < kV; ++i)
-          pb[i][sp] = load_f4(pres, sp < n_split && (threadIdx.x + i * 256) * 16u < row_bytes
-                                        ? sp * plane_bytes + prow + (threadIdx.x + i * 256) * 16u
+          pb[i][sp] = load_f4(pres, sp < n_split && (threadIdx.x + i * TH) * 16u < row_bytes
+                                        ? sp * plane_bytes + prow + (threadIdx.x + i * TH) * 16u
                                         : 0x80000000u);
 #pragma unroll
       for (int i = 0; i < kV; ++i) {
-        const int64_t j = threadIdx.x + i * 256;
+        const int64_t j = threadIdx.x + i * TH;
         float4 a = pb[i][0];
 #pragma unroll
         for (int sp = 1; sp < kPb; ++sp)
@@ -105,23 +108,31 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
       s += (a + b) + (c + d);
     }
   } else {
-    for (int64_t i = threadIdx.x; i < D; i += 256) {
+    for (int64_t i = threadIdx.x; i < D; i += TH) {
       const float t = xr[i];
       const float sq = t * t;
       s += sq;
     }
   }
   s = group_sum<64>(s);
-  __shared__ float part[4];
+  __shared__ float part[kW];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
-  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  // wave sums added as a pairwise tree in wave order
+  float t4[kW];
+#pragma unroll
+  for (int q = 0; q < kW; ++q) t4[q] = part[q];
+#pragma unroll
+  for (int w2 = kW / 2; w2 >= 1; w2 /= 2)
+#pragma unroll
+    for (int q = 0; q < w2; ++q) t4[q] = t4[2 * q] + t4[2 * q + 1];
+  const float total = t4[0];
   const float mean = total / static_cast<float>(D);
   const float r = 1.0f / sqrtf(mean + eps);
   if (vec) {
 #pragma unroll
     for (int i = 0; i < kV; ++i) {
-      const int64_t j = threadIdx.x + i * 256;
+      const int64_t j = threadIdx.x + i * TH;
       if (j < D / 4) {
         const float4 ww = wv[i];
         const float4 y =
@@ -140,7 +151,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
       }
     }
   } else {
-    for (int64_t i = threadIdx.x; i < D; i += 256) {
+    for (int64_t i = threadIdx.x; i < D; i += TH) {
       const float t = xr[i] * r;
       const float y = t * w[i];
       if (xh) store_x_planes(xh, xl, static_cast<int64_t>(blockIdx.x) * D + i, y);
@@ -450,12 +461,14 @@ int rmsnorm_planes(float* x, const float* w, uint16_t* xh, uint16_t* xl, int64_t
   if (n_split > 0 && (!part || !aligned(part, 16) || !rmsnorm_takes_partials(D) ||
                       static_cast<int64_t>(n_split) * M * D * 4 >= (int64_t{1} << 31)))
     return Q4_ERR_UNSUPPORTED;
+  // 1024 threads per row: each thread holds one float4 of the row and its partials, so a row's loads
+  // are spread over 16 waves instead of 4
   if (n_split > 6)
-    hipLaunchKernelGGL(rmsnorm_kernel<12>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
-                       nullptr, xh, xl, part, n_split);
+    hipLaunchKernelGGL((rmsnorm_kernel<12, 1024>), dim3(static_cast<unsigned>(M)), dim3(1024), 0, st, x, w, nullptr, M,
+                       D, eps, nullptr, xh, xl, part, n_split);
   else
-    hipLaunchKernelGGL(rmsnorm_kernel<6>, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, x, w, nullptr, M, D, eps,
-                       nullptr, xh, xl, part, n_split);
+    hipLaunchKernelGGL((rmsnorm_kernel<6, 1024>), dim3(static_cast<unsigned>(M)), dim3(1024), 0, st, x, w, nullptr, M,
+                       D, eps, nullptr, xh, xl, part, n_split);
   return launch_status();
 }
 
