@@ -569,7 +569,7 @@ def cpu_decode_baseline(pc, host_tensors, token, pos=700, L=1024, max_steps=3, b
                       "dequant of every int4 weight (eager QLinear.forward), same quantized weights"}
 
 
-def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
+def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5, runs=5, native_runs=3):
     import statistics
     import torch
     from q4llm import llm_runner, synth
@@ -584,7 +584,14 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
     prompt = synth.prompt_ids(512, synth.LLAMA32_3B["vocab_size"], seed=0)
     buckets = [256, 512, 1024, 2048, 4096]
     caches = model.new_caches()
-    res = llm_runner.run(model, prompt, n_new, 256, buckets, caches=caches)
+    # `runs` whole generations (prefill + decode, each after the runner's own warm-up); the tok/s
+    # figures are their medians, and every run must produce the same tokens
+    results = [llm_runner.run(model, prompt, n_new, 256, buckets, caches=caches) for _ in range(runs)]
+    res = results[-1]
+    if any(r["tokens"] != res["tokens"] for r in results):
+        raise RuntimeError("e2e: repeated generations produced different tokens")
+    pf_runs = sorted(r["prefill_tok_s"] for r in results)
+    dc_runs = sorted(r["decode_tok_s"] for r in results)
     # GPU-only time of one decode step at the bucket the run used: graph replays back to back, the
     # median and minimum over `reps` repetitions of 50 replays
     g = model.entry_point(1, 1024, caches)
@@ -608,10 +615,13 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
     avg_valid = 512 + (n_new - 1) / 2 + 1
     kv_valid = n_layers * 2 * avg_valid * 8 * 128 * 2
     kv_bucket = n_layers * 2 * 1024 * 8 * 128 * 2
-    tok_s = res["decode_tok_s"]
+    tok_s = statistics.median(dc_runs)
+    pf_tok_s = statistics.median(pf_runs)
     pf_flops, pf_roof = prefill_roofline_3b(len(prompt), 256)
     out = {
-        "decode_tok_s": tok_s, "prefill_tok_s": res["prefill_tok_s"], "ttft_ms": res["ttft_ms"],
+        "runs": runs, "decode_tok_s": round(tok_s, 2), "decode_tok_s_min_max": [dc_runs[0], dc_runs[-1]],
+        "prefill_tok_s": round(pf_tok_s, 1), "prefill_tok_s_min_max": [pf_runs[0], pf_runs[-1]],
+        "ttft_ms": statistics.median(r["ttft_ms"] for r in results),
         "decode_steps": res["decode_steps"], "gpu_ms_per_decode_step": round(gpu_ms, 4),
         "gpu_ms_per_decode_step_min": round(min(per), 4), "gpu_only_tok_s": round(1e3 / gpu_ms, 1),
         "bytes_per_step_valid_kv": int(w_bytes + kv_valid), "bytes_per_step_bucket_L1024": int(w_bytes + kv_bucket),
@@ -619,12 +629,13 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
         "frac_hbm_roofline": round(tok_s * (w_bytes + kv_valid) / (HBM_PEAK_GBS * 1e9), 4),
         "frac_hbm_roofline_gpu_only": round((w_bytes + kv_valid) / (gpu_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "prefill_flops_per_token": round(pf_flops), "prefill_roofline_tok_s": round(pf_roof, 1),
-        "frac_prefill_roofline": round(res["prefill_tok_s"] / pf_roof, 4),
+        "frac_prefill_roofline": round(pf_tok_s / pf_roof, 4),
         "tokens_sha1": hashlib.sha1(json.dumps(res["tokens"]).encode()).hexdigest(),
         "first_tokens": res["tokens"][:16], "model_build_s": round(build_s, 1),
         "buckets_used": sorted({L for L, _ in res["steps"]}),
     }
-    log(f"e2e decode {tok_s:.1f} tok/s (GPU-only {1e3 / gpu_ms:.1f}), prefill {res['prefill_tok_s']:.0f} tok/s")
+    log(f"e2e decode {tok_s:.1f} tok/s (GPU-only {1e3 / gpu_ms:.1f}), prefill {pf_tok_s:.0f} tok/s "
+        f"(medians of {runs} runs)")
     host = None
     if cpu:
         host = {k: v.cpu() for k, v in model.packed_tensors().items()}
@@ -643,11 +654,17 @@ def bench_e2e(dev, n_new=256, native=True, cpu=True, reps=5):
             model.save_packed(wpath)
             del model, caches, g
             torch.cuda.empty_cache()
-            nat = sweep.run_runner(wpath, prompt, n_new, 256, ",".join(map(str, buckets)), "bucketed")
-        out.update(native_runner_decode_tok_s=nat["decode_tok_s"], native_runner_prefill_tok_s=nat["prefill_tok_s"],
-                   native_runner_ttft_ms=nat["ttft_ms"], native_runner_tokens_match=nat["tokens"] == res["tokens"])
-        log(f"e2e native runner: decode {nat['decode_tok_s']:.1f} tok/s, prefill {nat['prefill_tok_s']:.0f} tok/s, "
-            f"tokens match: {nat['tokens'] == res['tokens']}")
+            nats = [sweep.run_runner(wpath, prompt, n_new, 256, ",".join(map(str, buckets)), "bucketed")
+                    for _ in range(native_runs)]
+        match = all(n["tokens"] == res["tokens"] for n in nats)
+        nat_dc = statistics.median(n["decode_tok_s"] for n in nats)
+        nat_pf = statistics.median(n["prefill_tok_s"] for n in nats)
+        out.update(native_runner_runs=native_runs, native_runner_decode_tok_s=nat_dc,
+                   native_runner_prefill_tok_s=nat_pf,
+                   native_runner_ttft_ms=statistics.median(n["ttft_ms"] for n in nats),
+                   native_runner_tokens_match=match)
+        log(f"e2e native runner: decode {nat_dc:.1f} tok/s, prefill {nat_pf:.0f} tok/s (medians of {native_runs} "
+            f"runs), tokens match: {match}")
     else:
         del model, caches, g
         torch.cuda.empty_cache()
