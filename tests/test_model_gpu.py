@@ -80,6 +80,21 @@ def test_tiny_generation_matches_golden(dev, variant):
     assert res["new_tokens"] == gold["max_new_tokens"] and res["decode_steps"] == gold["max_new_tokens"] - 1
 
 
+def test_generation_fills_the_context(dev):
+    """A prompt and token budget that use the whole context (n_prompt + new == max_ctx, the runner's
+    limit, llm_runner.c:169-173): a ragged last chunk padded to the bucket, the decode steps up to the
+    last position the schedule reaches, in the largest bucket, and the oracle's tokens."""
+    model, ref = build_pair(synth.TINY, 32, 128)
+    prompt = synth.prompt_ids(100, 1024, seed=5)
+    want = R.generate(ref, prompt, 28, 16, [64, 128])
+    res = llm_runner.run(model, prompt, 28, 16, [64, 128])
+    assert res["tokens"] == want
+    assert [L for L, _ in res["chunks"]] == [64, 64, 64, 64, 128, 128, 128]
+    assert res["decode_steps"] == 27 and {L for L, _ in res["steps"]} == {128}
+    with pytest.raises(llm_runner.RunnerError, match="exceeds max_ctx"):
+        llm_runner.run(model, prompt, 29, 16, [64, 128])
+
+
 def test_runner_ragged_prompt_and_stop_ids(dev):
     model, ref = build_pair(synth.TINY, 32, 128)
     prompt = synth.prompt_ids(21, 1024, seed=3)
