@@ -27,7 +27,7 @@ __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off
   return make_float4(f.x, f.y, f.z, f.w);
 }
 
-// rms_norm: one workgroup (256 threads) per row. x*x is rounded before the sum (x.pow(2)), the
+// rms_norm: one workgroup (TH threads) per row. x*x is rounded before the sum (x.pow(2)), the
 // mean is sum / D, r = 1 / sqrt(mean + eps) (both correctly rounded), out = (x * r) * w. Rows of at
 // most 4096 values (D % 4 == 0) are held in registers, loaded with all 16-byte loads in flight; the
 // norm weights are loaded with them, so no memory round trip follows the row reduction.
@@ -37,7 +37,7 @@ __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off
 // linear_reduce_kernel, so the same bits), and the completed row is written back to x. The first PB
 // partials load with the row, the rest one round trip each (PB 12 for more than 6 partials: the 128-row
 // prefill chunks have 8 and 10; 6 otherwise, where the 12-wide form measured 1.3% slower prefill).
-// TH threads per workgroup (256 or 1024), each holding 1024 / TH float4s of the row.
+// TH is 256, or 1024 for the prefill planes; each thread holds 1024 / TH float4s of the row.
 template <int PB = 6, int TH = 256>
 __global__ __launch_bounds__(TH) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
                                                       float* __restrict__ out, int64_t M, int64_t D, float eps,
